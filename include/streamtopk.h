@@ -1,0 +1,95 @@
+/*
+ * streamtopk.h -- C ABI of libstreamtopk_hip.so, the MI355X (gfx950) streaming
+ * fused top-k SAE encoder.
+ *
+ * It replaces the reference's pybind11 module `streamtopk_sae_native`
+ * (streamtopk_sae/csrc/bindings.cpp:28-51) and the CUDA/C++ sources behind it.
+ * Plain pointers and sizes only: the caller owns every buffer (inputs, outputs
+ * and the device workspace), so the library never allocates device memory.
+ *
+ * Conventions shared by every entry point:
+ *   - Return 0 on success; a non-zero STK_E_* code on failure, with a
+ *     thread-local message from stk_last_error().  Argument errors carry the
+ *     reference's TORCH_CHECK wording (streamtopk_exact.cu:794-830,
+ *     streamtopk_approx.cu:243-284, streamtopk_cpu.cpp:87-122).
+ *   - X is (B, d) row-major, W is (F, d) row-major, both of `dtype`; b is (F,)
+ *     fp32.  V is (B, k) fp32 and I is (B, k) int32, each row sorted by value
+ *     descending; equal values are ordered by lower latent index first.
+ *   - Device entry points run asynchronously on `stream` (a hipStream_t, NULL
+ *     for the legacy default stream) on the current HIP device; all pointers
+ *     must be device pointers on that device, 16-byte aligned.
+ */
+#ifndef STREAMTOPK_H
+#define STREAMTOPK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define STK_ABI_VERSION 1
+
+/* dtype codes for X and W */
+#define STK_DTYPE_F32 0
+#define STK_DTYPE_F16 1
+#define STK_DTYPE_BF16 2
+
+/* return codes */
+#define STK_OK 0
+#define STK_E_INVALID 1      /* argument rejected before any device work */
+#define STK_E_HIP 2          /* a HIP runtime call or launch failed */
+#define STK_E_WORKSPACE 3    /* workspace missing or smaller than required */
+
+/* ABI version of the loaded library (STK_ABI_VERSION it was built with). */
+int stk_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* stk_last_error(void);
+
+/* Device workspace (bytes) that stk_exact_forward needs for this problem on
+ * the current device.  Replaces the temporaries the reference allocates with
+ * libtorch inside launch_exact (streamtopk_exact.cu:686-689). */
+int stk_exact_workspace_bytes(int64_t B, int64_t d, int64_t F, int64_t k, int dtype,
+                              size_t* out_bytes);
+
+/* Exact encode: V, I = top_k(X @ W.T + b, k) without a (B, F) buffer.
+ * Replaces streamtopk_cuda_exact_forward (streamtopk_exact.cu:788-833),
+ * bound in the reference at bindings.cpp:33 and called from ops.py:57.
+ * k must be one of 1,2,4,8,16,32,64,128 and <= F; d <= 4096; d must be a
+ * multiple of 8 (fp16/bf16) or 4 (fp32). */
+int stk_exact_forward(const void* X, const void* W, const float* b, float* V, int32_t* I,
+                      int64_t B, int64_t d, int64_t F, int64_t k, int dtype,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* Device workspace (bytes) for stk_approx_forward.  `with_candidates` is
+ * non-zero when the caller passes a candidate buffer. */
+int stk_approx_workspace_bytes(int64_t B, int64_t d, int64_t F, int64_t k, int64_t c, int dtype,
+                               int with_candidates, size_t* out_bytes);
+
+/* Approximate encode: top-k of the union of each 128-latent group's top-c.
+ * Replaces streamtopk_cuda_approx_forward (streamtopk_approx.cu:234-291) plus
+ * the final torch.topk/gather the reference runs in Python (ops.py:75-81).
+ * c must be one of 16,32,64,128 and k <= c.  cand_vals / cand_idxs are
+ * optional (B, ceil(F/128), c) outputs (NULL to skip): each group's top-c,
+ * descending, padded with (-FLT_MAX, -1) -- the reference's candidate_buffer
+ * side effect (streamtopk_approx.cu:264-274). */
+int stk_approx_forward(const void* X, const void* W, const float* b, float* V, int32_t* I,
+                       int64_t B, int64_t d, int64_t F, int64_t k, int64_t c, int dtype,
+                       float* cand_vals, int32_t* cand_idxs,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* CPU encode on host memory, fp32 only, OpenMP over rows (num_threads <= 0:
+ * the OpenMP default).  Replaces streamtopk_cpu_forward
+ * (streamtopk_cpu.cpp:81-125), bound at bindings.cpp:29 and called from
+ * ops.py:40.  Output rows are sorted descending (the reference leaves k=128
+ * rows in heap order, topk_buffer.hpp:9). */
+int stk_cpu_forward(const float* X, const float* W, const float* b, float* V, int32_t* I,
+                    int64_t B, int64_t d, int64_t F, int64_t k, int num_threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STREAMTOPK_H */

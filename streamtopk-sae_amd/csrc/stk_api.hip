@@ -1,0 +1,356 @@
+// stk_api.hip -- the C ABI (include/streamtopk.h): argument validation with the
+// reference's error wording, launch planning for the current device, and the
+// kernel sequence of each entry point.  No device memory is allocated here:
+// every temporary lives in the caller's workspace.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/streamtopk.h"
+#include "stk_internal.h"
+#include "stk_kernels.h"
+
+namespace stk {
+
+static thread_local std::string g_err;
+
+int set_error(int code, const char* fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+void clear_error() { g_err.clear(); }
+
+bool k_supported(int64_t k)
+{
+    return k == 1 || k == 2 || k == 4 || k == 8 || k == 16 || k == 32 || k == 64 || k == 128;
+}
+
+static int hip_fail(hipError_t e, const char* what)
+{
+    return set_error(STK_E_HIP, "%s failed: %s", what, hipGetErrorString(e));
+}
+
+// Compute units of the current device (queried once per device).
+static int cu_count(int* out)
+{
+    static int cache[64] = {0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev >= 0 && dev < 64 && cache[dev] > 0) { *out = cache[dev]; return 0; }
+    int n = 0;
+    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
+    if (n <= 0) n = 1;
+    if (dev >= 0 && dev < 64) cache[dev] = n;
+    *out = n;
+    return 0;
+}
+
+static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+static int ilog2_floor(int64_t x) { int l = 0; while ((x >> (l + 1)) > 0) ++l; return l; }
+
+// ---------------------------------------------------------------------------
+// Exact-path plan
+// ---------------------------------------------------------------------------
+struct ExactPlan {
+    int NB, cap;
+    int64_t nbc, num_tiles, tpw;
+    int nwg;
+    bool sample;
+    int64_t samp_count;
+    int samp_log2;
+    int sNB;
+    int64_t s_nbc, s_gx, spp;
+    int nsplit;
+    size_t off_seed, off_thr, off_P, off_keys, off_cnt, total;
+};
+
+static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int dtype, int ncu)
+{
+    ExactPlan p;
+    const int64_t DS = (dtype == STK_DTYPE_F32) ? 32 : 64;
+    const int64_t nds = cdiv(d, DS);
+    const int64_t bblocks = cdiv(B > 0 ? B : 1, 32);
+    const int64_t nb_max = (k > 64) ? 2 : 4;   // k=128 queues need the LDS of 64 rows
+    p.NB = (int)(bblocks < nb_max ? bblocks : nb_max);
+    if (p.NB == 3) p.NB = 4;
+    p.cap = (int)(k + 32);
+    if (p.cap & 1) ++p.cap;
+    p.nbc = cdiv(B, 32 * p.NB);
+    p.num_tiles = cdiv(F, kTileLatents);
+    int64_t nwg = ncu / (p.nbc > 0 ? p.nbc : 1);
+    if (nwg < 1) nwg = 1;
+    if (nwg > p.num_tiles) nwg = p.num_tiles;
+    p.tpw = cdiv(p.num_tiles, nwg);
+    p.nwg = (int)cdiv(p.num_tiles, p.tpw);
+
+    p.sample = F >= kSampleMinF;
+    p.samp_count = 0;
+    p.samp_log2 = 0;
+    p.sNB = p.NB;
+    p.s_nbc = p.s_gx = p.spp = 0;
+    p.nsplit = 0;
+    if (p.sample) {
+        int l = ilog2_floor(F / kSampleTarget);
+        if (l < 4) l = 4;
+        p.samp_log2 = l;
+        p.samp_count = F >> l;
+        if (p.samp_count > kSampleTarget) p.samp_count = kSampleTarget;
+        p.sNB = (int)(bblocks < 4 ? bblocks : 4);
+        if (p.sNB == 3) p.sNB = 4;
+        p.s_nbc = cdiv(B, 32 * p.sNB);
+        p.s_gx = cdiv(p.samp_count, 128);
+        int64_t ns = ncu / (p.s_gx * p.s_nbc);
+        if (ns < 1) ns = 1;
+        if (ns > nds) ns = nds;
+        p.spp = cdiv(nds, ns);
+        p.nsplit = (int)cdiv(nds, p.spp);
+    }
+    size_t off = 0;
+    p.off_seed = off;
+    if (p.sample) off = align256(off + (size_t)B * k * 8);
+    p.off_thr = off;
+    if (p.sample) off = align256(off + (size_t)B * 8);
+    p.off_P = off;
+    if (p.sample) off = align256(off + (size_t)p.nsplit * B * p.samp_count * 4);
+    p.off_keys = off;
+    off = align256(off + (size_t)B * p.nwg * p.cap * 8);
+    p.off_cnt = off;
+    off = align256(off + (size_t)B * p.nwg * 4);
+    p.total = off;
+    return p;
+}
+
+static int check_dtype(int dtype)
+{
+    if (dtype != STK_DTYPE_F32 && dtype != STK_DTYPE_F16 && dtype != STK_DTYPE_BF16)
+        return set_error(STK_E_INVALID, "X dtype must be fp32, fp16, or bf16");
+    return 0;
+}
+
+static int check_shape_common(int64_t B, int64_t d, int64_t F, int dtype)
+{
+    if (B < 0 || d < 1 || F < 1) return set_error(STK_E_INVALID, "invalid shape: B=%lld d=%lld F=%lld",
+                                                  (long long)B, (long long)d, (long long)F);
+    if (F > 0x7FFFFFFELL) return set_error(STK_E_INVALID, "F=%lld exceeds the int32 index range", (long long)F);
+    const int64_t q = (dtype == STK_DTYPE_F32) ? 4 : 8;
+    if (d % q)
+        return set_error(STK_E_INVALID,
+                         "d=%lld must be a multiple of %lld for %s inputs (pad X and W_enc with zero columns)",
+                         (long long)d, (long long)q, dtype == STK_DTYPE_F32 ? "fp32" : "fp16/bf16");
+    return 0;
+}
+
+static int check_ptrs(const void* X, const void* W, const void* b, const void* V, const void* I)
+{
+    if (!X || !W || !b || !V || !I) return set_error(STK_E_INVALID, "null tensor pointer");
+    if (((uintptr_t)X | (uintptr_t)W) & 15) return set_error(STK_E_INVALID, "X and W_enc must be 16-byte aligned");
+    if ((uintptr_t)b & 3) return set_error(STK_E_INVALID, "b_enc must be 4-byte aligned");
+    return 0;
+}
+
+static int validate_exact(int64_t B, int64_t d, int64_t F, int64_t k, int dtype)
+{
+    int rc;
+    if ((rc = check_dtype(dtype))) return rc;
+    if (B < 0 || d < 1 || F < 1) return check_shape_common(B, d, F, dtype);
+    if (k < 1 || k > F) return set_error(STK_E_INVALID, "k out of range");
+    if (d > 4096) return set_error(STK_E_INVALID, "d exceeds D_MAX=4096");
+    if (!k_supported(k))
+        return set_error(STK_E_INVALID, "streamtopk_cuda_exact: unsupported k=%lld. Supported: 1,2,4,8,16,32,64,128.",
+                         (long long)k);
+    return check_shape_common(B, d, F, dtype);
+}
+
+// Runs sample -> seed -> main -> merge on `st`.
+static int run_exact(const ExactPlan& p, const void* X, const void* W, const float* b, float* V, int32_t* I,
+                     int64_t B, int64_t d, int64_t F, int64_t k, int dtype, unsigned char* ws, hipStream_t st)
+{
+    const int dt = dtype;   // STK_DTYPE_* and DT_* share values
+    hipError_t e;
+    uint64_t* seed = (uint64_t*)(ws + p.off_seed);
+    uint64_t* thr = (uint64_t*)(ws + p.off_thr);
+    if (p.sample) {
+        SampleArgs sa;
+        sa.X = X; sa.W = W; sa.B = B; sa.d = d;
+        sa.count = p.samp_count; sa.samp_log2 = p.samp_log2;
+        sa.steps_per_split = p.spp;
+        sa.P = (float*)(ws + p.off_P);
+        e = launch_sample(dt, p.sNB, sa, dim3((unsigned)p.s_gx, (unsigned)p.nsplit, (unsigned)p.s_nbc), st);
+        if (e != hipSuccess) return hip_fail(e, "sample_kernel launch");
+        SeedArgs sd;
+        sd.P = sa.P; sd.bias = b; sd.B = B; sd.count = p.samp_count;
+        sd.nsplit = p.nsplit; sd.samp_log2 = p.samp_log2; sd.k = (int)k;
+        sd.seed_keys = seed; sd.thr = thr;
+        e = launch_seed(sd, B, st);
+        if (e != hipSuccess) return hip_fail(e, "seed_kernel launch");
+    }
+    MainArgs ma;
+    ma.X = X; ma.W = W; ma.bias = b; ma.B = B; ma.d = d; ma.F = F;
+    ma.k = (int)k; ma.cap = p.cap;
+    ma.num_tiles = p.num_tiles; ma.tiles_per_wg = p.tpw; ma.nwg = p.nwg;
+    ma.thr0 = p.sample ? thr : nullptr;
+    ma.samp_count = p.sample ? p.samp_count : 0;
+    ma.samp_log2 = p.samp_log2;
+    ma.out_keys = (uint64_t*)(ws + p.off_keys);
+    ma.out_cnt = (int32_t*)(ws + p.off_cnt);
+    e = launch_main(dt, p.NB, ma, dim3((unsigned)p.nwg, (unsigned)p.nbc), st);
+    if (e != hipSuccess) return hip_fail(e, "main_kernel launch");
+    MergeArgs mg;
+    mg.seed_keys = p.sample ? seed : nullptr;
+    mg.seg_keys = ma.out_keys; mg.seg_cnt = ma.out_cnt;
+    mg.nseg = p.nwg; mg.cap = p.cap; mg.k = (int)k;
+    mg.V = V; mg.I = I;
+    e = launch_merge(mg, B, st);
+    if (e != hipSuccess) return hip_fail(e, "merge_kernel launch");
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Approximate-path plan (candidate buffer requested)
+// ---------------------------------------------------------------------------
+struct GroupPlan {
+    int NB;
+    int64_t nbc, num_groups, tpw;
+    int nwg;
+};
+
+static GroupPlan make_group_plan(int64_t B, int64_t F, int ncu)
+{
+    GroupPlan p;
+    const int64_t bblocks = cdiv(B > 0 ? B : 1, 32);
+    p.NB = (int)(bblocks < 4 ? bblocks : 4);
+    if (p.NB == 3) p.NB = 4;
+    p.nbc = cdiv(B, 32 * p.NB);
+    p.num_groups = cdiv(F, kApproxGroup);
+    const int64_t num_tiles = cdiv(p.num_groups, 2);
+    int64_t nwg = ncu / (p.nbc > 0 ? p.nbc : 1);
+    if (nwg < 1) nwg = 1;
+    if (nwg > num_tiles) nwg = num_tiles;
+    p.tpw = cdiv(num_tiles, nwg);
+    p.nwg = (int)cdiv(num_tiles, p.tpw);
+    return p;
+}
+
+static int validate_approx(int64_t B, int64_t d, int64_t F, int64_t k, int64_t c, int dtype)
+{
+    int rc;
+    if ((rc = check_dtype(dtype))) return rc;
+    if (k < 1 || k > c) return set_error(STK_E_INVALID, "k must be <= c");
+    if (c != 16 && c != 32 && c != 64 && c != 128)
+        return set_error(STK_E_INVALID, "streamtopk_cuda_approx: unsupported c=%lld. Supported: 16,32,64,128.",
+                         (long long)c);
+    if ((rc = check_shape_common(B, d, F, dtype))) return rc;
+    if (k > F) return set_error(STK_E_INVALID, "k out of range");
+    return 0;
+}
+
+}  // namespace stk
+
+using namespace stk;
+
+extern "C" {
+
+int stk_abi_version(void) { return STK_ABI_VERSION; }
+
+const char* stk_last_error(void) { return g_err.c_str(); }
+
+int stk_exact_workspace_bytes(int64_t B, int64_t d, int64_t F, int64_t k, int dtype, size_t* out_bytes)
+{
+    clear_error();
+    if (!out_bytes) return set_error(STK_E_INVALID, "null out_bytes");
+    int rc = validate_exact(B, d, F, k, dtype);
+    if (rc) return rc;
+    int ncu = 0;
+    if ((rc = cu_count(&ncu))) return rc;
+    *out_bytes = (B == 0) ? 0 : make_exact_plan(B, d, F, k, dtype, ncu).total;
+    return 0;
+}
+
+int stk_exact_forward(const void* X, const void* W, const float* b, float* V, int32_t* I,
+                      int64_t B, int64_t d, int64_t F, int64_t k, int dtype,
+                      void* workspace, size_t workspace_bytes, void* stream)
+{
+    clear_error();
+    int rc = validate_exact(B, d, F, k, dtype);
+    if (rc) return rc;
+    if (B == 0) return 0;
+    if ((rc = check_ptrs(X, W, b, V, I))) return rc;
+    int ncu = 0;
+    if ((rc = cu_count(&ncu))) return rc;
+    const ExactPlan p = make_exact_plan(B, d, F, k, dtype, ncu);
+    if (!workspace || workspace_bytes < p.total)
+        return set_error(STK_E_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required",
+                         workspace ? workspace_bytes : (size_t)0, p.total);
+    if ((uintptr_t)workspace & 255) return set_error(STK_E_INVALID, "workspace must be 256-byte aligned");
+    return run_exact(p, X, W, b, V, I, B, d, F, k, dtype, (unsigned char*)workspace, (hipStream_t)stream);
+}
+
+int stk_approx_workspace_bytes(int64_t B, int64_t d, int64_t F, int64_t k, int64_t c, int dtype,
+                               int with_candidates, size_t* out_bytes)
+{
+    clear_error();
+    if (!out_bytes) return set_error(STK_E_INVALID, "null out_bytes");
+    int rc = validate_approx(B, d, F, k, c, dtype);
+    if (rc) return rc;
+    if (with_candidates || B == 0) { *out_bytes = 0; return 0; }
+    int ncu = 0;
+    if ((rc = cu_count(&ncu))) return rc;
+    *out_bytes = make_exact_plan(B, d, F, k, dtype, ncu).total;
+    return 0;
+}
+
+int stk_approx_forward(const void* X, const void* W, const float* b, float* V, int32_t* I,
+                       int64_t B, int64_t d, int64_t F, int64_t k, int64_t c, int dtype,
+                       float* cand_vals, int32_t* cand_idxs,
+                       void* workspace, size_t workspace_bytes, void* stream)
+{
+    clear_error();
+    int rc = validate_approx(B, d, F, k, c, dtype);
+    if (rc) return rc;
+    if (B == 0) return 0;
+    if ((rc = check_ptrs(X, W, b, V, I))) return rc;
+    if ((cand_vals == nullptr) != (cand_idxs == nullptr))
+        return set_error(STK_E_INVALID, "cand_vals and cand_idxs must both be given or both be NULL");
+    int ncu = 0;
+    if ((rc = cu_count(&ncu))) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    if (cand_vals == nullptr) {
+        // With k <= c, every one of the k best latents of a row is within the
+        // top-c of its own group (fewer than k <= c latents of the row beat
+        // it), so the union of the per-group top-c holds the exact top-k and
+        // its top-k is exactly that set: the exact streaming path computes the
+        // approximate result without materialising any candidate.
+        const ExactPlan p = make_exact_plan(B, d, F, k, dtype, ncu);
+        if (!workspace || workspace_bytes < p.total)
+            return set_error(STK_E_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required",
+                             workspace ? workspace_bytes : (size_t)0, p.total);
+        if ((uintptr_t)workspace & 255) return set_error(STK_E_INVALID, "workspace must be 256-byte aligned");
+        return run_exact(p, X, W, b, V, I, B, d, F, k, dtype, (unsigned char*)workspace, st);
+    }
+    const GroupPlan p = make_group_plan(B, F, ncu);
+    GroupArgs ga;
+    ga.X = X; ga.W = W; ga.bias = b; ga.B = B; ga.d = d; ga.F = F; ga.c = (int)c;
+    ga.num_groups = p.num_groups; ga.tiles_per_wg = p.tpw;
+    ga.cand_vals = cand_vals; ga.cand_idxs = cand_idxs;
+    hipError_t e = launch_group(dtype, p.NB, ga, dim3((unsigned)p.nwg, (unsigned)p.nbc), st);
+    if (e != hipSuccess) return hip_fail(e, "group_kernel launch");
+    CandArgs ca;
+    ca.cand_vals = cand_vals; ca.cand_idxs = cand_idxs;
+    ca.per_row = p.num_groups * c; ca.k = (int)k; ca.V = V; ca.I = I;
+    e = launch_cand(ca, B, st);
+    if (e != hipSuccess) return hip_fail(e, "cand_kernel launch");
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,87 @@
+// stk_kernels.h -- kernel argument blocks and host launch helpers shared by
+// the kernels (stk_kernels.hip, stk_approx.hip) and the C ABI (stk_api.hip).
+#pragma once
+#include "stk_select.h"
+
+namespace stk {
+
+constexpr int kTileLatents = 256;    // latents per main_kernel tile (4 waves x 64)
+constexpr int kApproxGroup = 128;    // latent group of the approximate variant
+constexpr int kSampleTarget = 4096;  // sampled latents that seed the thresholds
+constexpr int64_t kSampleMinF = 16384;
+
+struct MainArgs {
+    const void* X;
+    const void* W;
+    const float* bias;
+    int64_t B, d, F;
+    int k, cap;
+    int64_t num_tiles, tiles_per_wg;
+    int nwg;
+    const uint64_t* thr0;        // per-row starting threshold keys, or null
+    int64_t samp_count;          // latents f = i << samp_log2, i < samp_count, are
+    int samp_log2;               //   scored by the sample pass and skipped here
+    uint64_t* out_keys;          // [B][nwg][cap]
+    int32_t* out_cnt;            // [B][nwg]
+};
+
+struct SampleArgs {
+    const void* X;
+    const void* W;
+    int64_t B, d;
+    int64_t count;
+    int samp_log2;
+    int64_t steps_per_split;
+    float* P;                    // [nsplit][B][count]
+};
+
+struct SeedArgs {
+    const float* P;
+    const float* bias;
+    int64_t B, count;
+    int nsplit, samp_log2, k;
+    uint64_t* seed_keys;         // [B][k], descending
+    uint64_t* thr;               // [B]
+};
+
+struct MergeArgs {
+    const uint64_t* seed_keys;   // [B][k] or null
+    const uint64_t* seg_keys;    // [B][nseg][cap]
+    const int32_t* seg_cnt;      // [B][nseg]
+    int64_t nseg;
+    int cap, k;
+    float* V;
+    int32_t* I;
+};
+
+struct GroupArgs {               // approximate variant, per-group top-c candidates
+    const void* X;
+    const void* W;
+    const float* bias;
+    int64_t B, d, F;
+    int c;
+    int64_t num_groups, tiles_per_wg;
+    float* cand_vals;            // [B][num_groups][c]
+    int32_t* cand_idxs;          // [B][num_groups][c]
+};
+
+struct CandArgs {                // approximate variant, top-k over the candidates
+    const float* cand_vals;
+    const int32_t* cand_idxs;
+    int64_t per_row;             // num_groups * c
+    int k;
+    float* V;
+    int32_t* I;
+};
+
+size_t main_lds_bytes(int NB, int cap);
+size_t group_lds_bytes(int NB);
+
+hipError_t launch_main(int dt, int NB, const MainArgs& a, dim3 grid, hipStream_t st);
+hipError_t launch_sample(int dt, int NB, const SampleArgs& a, dim3 grid, hipStream_t st);
+hipError_t launch_seed(const SeedArgs& a, int64_t rows, hipStream_t st);
+hipError_t launch_merge(const MergeArgs& a, int64_t rows, hipStream_t st);
+hipError_t launch_group(int dt, int NB, const GroupArgs& a, dim3 grid, hipStream_t st);
+hipError_t launch_cand(const CandArgs& a, int64_t rows, hipStream_t st);
+
+}  // namespace stk

@@ -1,0 +1,182 @@
+"""Drop-in op surface of ``streamtopk_sae.ops`` (reference: streamtopk_sae/ops.py).
+
+Same names, arguments, dtype handling and error behaviour as the reference:
+
+* ``topk_sae_cpu(X, W_enc, b_enc, k)``                       (ops.py:23-40)
+* ``topk_sae_cuda_exact(X, W_enc, b_enc, k)``                (ops.py:43-57)
+* ``topk_sae_cuda_approx(X, W_enc, b_enc, k, c, candidate_buffer=None)``
+                                                             (ops.py:60-83)
+
+Each returns ``(values fp32 (B, k), indices int32 (B, k))``, rows sorted by
+value descending.  The device ops run the gfx950 kernels of
+``libstreamtopk_hip.so`` on the current stream of X's device; outputs and the
+workspace are allocated here with torch, so ``torch.cuda.max_memory_allocated``
+sees every byte and no (B, F) buffer is ever created.
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+
+_DTYPES = {
+    torch.float32: _lib.STK_DTYPE_F32,
+    torch.float16: _lib.STK_DTYPE_F16,
+    torch.bfloat16: _lib.STK_DTYPE_BF16,
+}
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _pad_d(X, W_enc, multiple):
+    """Zero-pad the reduction axis to `multiple` (exact: zeros add nothing)."""
+    d = X.shape[1]
+    pad = (-d) % multiple
+    if pad == 0:
+        return X, W_enc
+    X = torch.nn.functional.pad(X, (0, pad))
+    W_enc = torch.nn.functional.pad(W_enc, (0, pad))
+    return X.contiguous(), W_enc.contiguous()
+
+
+def _aligned(t):
+    """Contiguous tensor whose data pointer is 16-byte aligned."""
+    t = t.contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+def _device_checks(X, W_enc, b_enc, need_w_device=True):
+    # streamtopk_exact.cu:800-812 / streamtopk_approx.cu:246-258
+    if not X.is_cuda:
+        raise RuntimeError("X must be on CUDA")
+    if need_w_device and not W_enc.is_cuda:
+        raise RuntimeError("W_enc must be on CUDA")
+    if need_w_device and not b_enc.is_cuda:
+        raise RuntimeError("b_enc must be on CUDA")
+    if W_enc.device != X.device or b_enc.device != X.device:
+        raise RuntimeError("X, W_enc and b_enc must be on the same device")
+    if b_enc.dtype != torch.float32:
+        raise RuntimeError("b_enc must be fp32")
+    if X.dtype not in _DTYPES:
+        raise RuntimeError("X dtype must be fp32, fp16, or bf16")
+    if W_enc.dtype != X.dtype:
+        raise RuntimeError("W_enc dtype must match X")
+    if X.dim() != 2 or W_enc.dim() != 2 or b_enc.dim() != 1:
+        raise RuntimeError("expected X (B, d), W_enc (F, d), b_enc (F,)")
+    if W_enc.shape[1] != X.shape[1]:
+        raise RuntimeError("W_enc d-dim mismatch")
+    if b_enc.shape[0] != W_enc.shape[0]:
+        raise RuntimeError("b_enc F-dim mismatch")
+
+
+def topk_sae_cpu(X, W_enc, b_enc, k):
+    """CPU streaming top-k SAE forward (fp32; fp16/bf16 inputs are upcast).
+
+    Returns values (B, k) fp32 and indices (B, k) int32 on the CPU.
+    """
+    lib = _lib.load()
+    if X.dtype != torch.float32:
+        X = X.float()
+        W_enc = W_enc.float()
+    if b_enc.dtype != torch.float32:
+        b_enc = b_enc.float()
+    X = X.contiguous()
+    W_enc = W_enc.contiguous()
+    b_enc = b_enc.contiguous()
+    # streamtopk_cpu.cpp:87-99
+    if X.dtype != torch.float32:
+        raise RuntimeError("X must be fp32")
+    if W_enc.dtype != torch.float32:
+        raise RuntimeError("W_enc must be fp32")
+    if X.is_cuda or W_enc.is_cuda or b_enc.is_cuda:
+        raise RuntimeError("topk_sae_cpu expects CPU tensors")
+    if W_enc.shape[1] != X.shape[1]:
+        raise RuntimeError("W_enc d-dim mismatch")
+    if b_enc.shape[0] != W_enc.shape[0]:
+        raise RuntimeError("b_enc F-dim mismatch")
+    B, d = X.shape
+    F = W_enc.shape[0]
+    V = torch.empty((B, k), dtype=torch.float32) if k >= 1 else None
+    I = torch.empty((B, k), dtype=torch.int32) if k >= 1 else None
+    rc = lib.stk_cpu_forward(_ptr(X), _ptr(W_enc), _ptr(b_enc), _ptr(V), _ptr(I),
+                             B, d, F, k, 0)
+    _lib.check(rc)
+    return V, I
+
+
+def _prepare_device(X, W_enc, b_enc):
+    if b_enc.dtype != torch.float32:
+        b_enc = b_enc.float()
+    X = X.contiguous()
+    W_enc = W_enc.contiguous()
+    b_enc = b_enc.contiguous()
+    _device_checks(X, W_enc, b_enc)
+    multiple = 4 if X.dtype == torch.float32 else 8
+    X, W_enc = _pad_d(X, W_enc, multiple)
+    return _aligned(X), _aligned(W_enc), b_enc
+
+
+def topk_sae_cuda_exact(X, W_enc, b_enc, k):
+    """Exact streaming top-k SAE forward on the GPU (fp16, bf16, fp32; b_enc fp32).
+
+    Returns values (B, k) fp32 and indices (B, k) int32 on X's device.
+    """
+    lib = _lib.load()
+    X, W_enc, b_enc = _prepare_device(X, W_enc, b_enc)
+    B, d = X.shape
+    F = W_enc.shape[0]
+    dt = _DTYPES[X.dtype]
+    with torch.cuda.device(X.device):
+        nbytes = ctypes.c_size_t(0)
+        _lib.check(lib.stk_exact_workspace_bytes(B, d, F, k, dt, ctypes.byref(nbytes)))
+        V = torch.empty((B, k), dtype=torch.float32, device=X.device)
+        I = torch.empty((B, k), dtype=torch.int32, device=X.device)
+        ws = torch.empty(max(nbytes.value, 1), dtype=torch.uint8, device=X.device)
+        stream = torch.cuda.current_stream(X.device).cuda_stream
+        rc = lib.stk_exact_forward(_ptr(X), _ptr(W_enc), _ptr(b_enc), _ptr(V), _ptr(I),
+                                   B, d, F, k, dt, _ptr(ws), ws.numel(), ctypes.c_void_p(stream))
+        _lib.check(rc)
+    return V, I
+
+
+def topk_sae_cuda_approx(X, W_enc, b_enc, k, c, candidate_buffer=None):
+    """Approximate streaming top-k SAE forward: top-c per 128-latent group, then
+    top-k of the union.  c must be in {16, 32, 64, 128} and >= k.
+
+    If `candidate_buffer` (fp32, shape (B, ceil(F/128), c)) is given it is
+    filled with each group's top-c values, descending, padded with -FLT_MAX.
+    Returns values (B, k) fp32 and indices (B, k) int32.
+    """
+    lib = _lib.load()
+    X, W_enc, b_enc = _prepare_device(X, W_enc, b_enc)
+    B, d = X.shape
+    F = W_enc.shape[0]
+    dt = _DTYPES[X.dtype]
+    nt = (F + 127) // 128
+    with torch.cuda.device(X.device):
+        with_cand = candidate_buffer is not None
+        cand_vals = cand_idxs = None
+        if with_cand:
+            cb = candidate_buffer
+            if cb.dim() != 3 or tuple(cb.shape) != (B, nt, c):
+                raise RuntimeError("candidate_buffer shape mismatch")
+            if cb.dtype != torch.float32 or cb.device != X.device or not cb.is_contiguous():
+                raise RuntimeError("candidate_buffer must be a contiguous fp32 tensor on X's device")
+            cand_vals = cb
+            cand_idxs = torch.empty((B, nt, c), dtype=torch.int32, device=X.device)
+        nbytes = ctypes.c_size_t(0)
+        _lib.check(lib.stk_approx_workspace_bytes(B, d, F, k, c, dt, int(with_cand),
+                                                  ctypes.byref(nbytes)))
+        V = torch.empty((B, k), dtype=torch.float32, device=X.device)
+        I = torch.empty((B, k), dtype=torch.int32, device=X.device)
+        ws = torch.empty(max(nbytes.value, 1), dtype=torch.uint8, device=X.device)
+        stream = torch.cuda.current_stream(X.device).cuda_stream
+        rc = lib.stk_approx_forward(_ptr(X), _ptr(W_enc), _ptr(b_enc), _ptr(V), _ptr(I),
+                                    B, d, F, k, c, dt, _ptr(cand_vals), _ptr(cand_idxs),
+                                    _ptr(ws), ws.numel(), ctypes.c_void_p(stream))
+        _lib.check(rc)
+    return V, I

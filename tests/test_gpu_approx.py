@@ -1,0 +1,97 @@
+"""GPU parity of the approximate encoder (topk_sae_cuda_approx).
+
+Without a candidate buffer the result must equal the exact top-k (with k <= c
+every exact top-k latent is inside its group's top-c).  With a candidate
+buffer the per-group top-c values are compared with the oracle's candidates
+(streamtopk_approx.cu:118-166 semantics) and the final top-k with the
+oracle's approx result.  Recall tests mirror the reference's
+tests/test_recall.py:22-96.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from parity import check_against_scores
+from streamtopk_sae import make_inputs, recall_at_k, topk_sae_cuda_approx, topk_sae_cuda_exact
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+@pytest.mark.parametrize("c", [16, 32, 64, 128])
+def test_approx_equals_exact(cuda_dev, c):
+    print(f"case approx==exact c={c}", flush=True)
+    X, W, b = make_inputs(32, 256, 20000, torch.bfloat16, seed=21, device=cuda_dev)
+    k = 16
+    Va, Ia = topk_sae_cuda_approx(X, W, b, k, c)
+    Ve, Ie = topk_sae_cuda_exact(X, W, b, k)
+    assert torch.equal(Va, Ve) and torch.equal(Ia, Ie)
+    assert recall_at_k(Ia, Ie) == 1.0
+
+
+@pytest.mark.parametrize("c", [16, 32, 64, 128])
+@pytest.mark.parametrize("F", [256, 1000])
+def test_approx_candidate_buffer(cuda_dev, c, F):
+    print(f"case approx candidates c={c} F={F}", flush=True)
+    B, d, k = 8, 64, min(16, c)
+    X, W, b = make_inputs(B, d, F, torch.bfloat16, seed=22, device=cuda_dev)
+    nt = (F + 127) // 128
+    cb = torch.empty((B, nt, c), dtype=torch.float32, device=cuda_dev)
+    V, I = topk_sae_cuda_approx(X, W, b, k, c, candidate_buffer=cb)
+    Vo, Io, cvo, cio = oracle.approx(_np(X), _np(W), _np(b), k, c, with_candidates=True)
+    cbn = cb.cpu().numpy()
+    pad = cio < 0
+    assert np.array_equal(cbn[pad], cvo[pad])
+    err = np.abs(cbn[~pad] - cvo[~pad]) / np.maximum(np.abs(cvo[~pad]), 1.0)
+    assert err.max() <= 2e-3
+    S = oracle.scores_f64(_np(X), _np(W), _np(b))
+    check_against_scores(V.cpu().numpy(), I.cpu().numpy(), S, k, 2e-3, f"approx c={c}")
+
+
+def test_approx_candidate_buffer_final_matches_exact(cuda_dev):
+    X, W, b = make_inputs(16, 128, 5000, torch.bfloat16, seed=23, device=cuda_dev)
+    nt = (5000 + 127) // 128
+    cb = torch.empty((16, nt, 32), dtype=torch.float32, device=cuda_dev)
+    Va, Ia = topk_sae_cuda_approx(X, W, b, 32, 32, candidate_buffer=cb)
+    Ve, Ie = topk_sae_cuda_exact(X, W, b, 32)
+    assert torch.equal(Va, Ve) and torch.equal(Ia, Ie)
+
+
+@pytest.mark.parametrize("shape", [dict(B=32, d=256, F=1024, k=16), dict(B=32, d=256, F=2048, k=32)])
+def test_recall_monotonicity(cuda_dev, shape):
+    X, W, b = make_inputs(shape["B"], shape["d"], shape["F"], torch.bfloat16, seed=0, device=cuda_dev)
+    k = shape["k"]
+    _, ref_i = topk_sae_cuda_exact(X, W, b, k)
+    recalls = [recall_at_k(topk_sae_cuda_approx(X, W, b, k, c)[1], ref_i) for c in (16, 32, 64, 128) if c >= k]
+    for r0, r1 in zip(recalls, recalls[1:]):
+        assert r1 >= r0 - 0.02
+    assert all(r == 1.0 for r in recalls)
+
+
+def test_approx_errors(cuda_dev):
+    X, W, b = make_inputs(4, 64, 256, torch.bfloat16, seed=24, device=cuda_dev)
+    with pytest.raises(RuntimeError, match="k must be <= c"):
+        topk_sae_cuda_approx(X, W, b, 32, 16)
+    with pytest.raises(RuntimeError, match="unsupported c=48"):
+        topk_sae_cuda_approx(X, W, b, 8, 48)
+    with pytest.raises(RuntimeError, match="candidate_buffer shape mismatch"):
+        topk_sae_cuda_approx(X, W, b, 8, 16, candidate_buffer=torch.empty(4, 3, 16, device=cuda_dev))
+
+
+@pytest.mark.parametrize("with_buffer", [False, True])
+def test_approx_known_answers(cuda_dev, with_buffer):
+    from golden.make_golden import load as load_golden
+    for X, W, b, k, Vk, Ik in load_golden():
+        c = max(16, k)
+        Xt = torch.from_numpy(X).to(cuda_dev).bfloat16()
+        Wt = torch.from_numpy(W).to(cuda_dev).bfloat16()
+        bt = torch.from_numpy(b).to(cuda_dev)
+        cb = None
+        if with_buffer:
+            cb = torch.empty((X.shape[0], (W.shape[0] + 127) // 128, c), dtype=torch.float32, device=cuda_dev)
+        V, I = topk_sae_cuda_approx(Xt, Wt, bt, k, c, candidate_buffer=cb)
+        assert np.array_equal(V.cpu().numpy(), Vk) and np.array_equal(I.cpu().numpy(), Ik)

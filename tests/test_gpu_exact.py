@@ -1,0 +1,201 @@
+"""GPU parity of the exact encoder (topk_sae_cuda_exact -> stk_exact_forward).
+
+Small and medium shapes are checked against the C oracle's float64 scores;
+larger shapes against float64 scores computed on the GPU with torch (the same
+quantity, cross-checked against the oracle in test_torch_f64_scores_match_oracle);
+the full headline configuration through size-independent properties.
+Shapes and edge cases follow the reference's tests/test_correctness.py:16-293.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from parity import check_against_scores, tol_of
+from streamtopk_sae import make_inputs, topk_sae_cuda_exact
+
+pytestmark = pytest.mark.gpu
+
+DT = {"fp32": torch.float32, "fp16": torch.float16, "bf16": torch.bfloat16}
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _oracle_scores(X, W, b):
+    return oracle.scores_f64(_np(X), _np(W), _np(b))
+
+
+def _gpu_scores_f64(X, W, b):
+    return (X.double() @ W.double().T + b.double()).cpu().numpy()
+
+
+def _run_check(X, W, b, k, dtype_name, scores="oracle", name=""):
+    V, I = topk_sae_cuda_exact(X, W, b, k)
+    torch.cuda.synchronize()
+    assert V.dtype == torch.float32 and I.dtype == torch.int32
+    assert V.device == X.device and I.device == X.device
+    S = _oracle_scores(X, W, b) if scores == "oracle" else _gpu_scores_f64(X, W, b)
+    ties = check_against_scores(V.cpu().numpy(), I.cpu().numpy(), S, k, tol_of(dtype_name), name)
+    if ties:
+        print(f"[ties] {name}: {ties} row(s) with near-tie index differences")
+    return V, I
+
+
+SHAPES = {
+    "small": dict(B=4, d=64, F=256, k=8),
+    "medium": dict(B=32, d=512, F=4096, k=32),
+    "sampled": dict(B=64, d=256, F=20000, k=64),
+}
+
+
+@pytest.mark.parametrize("shape", list(SHAPES))
+@pytest.mark.parametrize("dtype_name", ["fp32", "fp16", "bf16"])
+def test_exact_shapes(cuda_dev, shape, dtype_name):
+    c = SHAPES[shape]
+    print(f"case exact {shape} {dtype_name} {c}", flush=True)
+    X, W, b = make_inputs(c["B"], c["d"], c["F"], DT[dtype_name], seed=42, device=cuda_dev)
+    _run_check(X, W, b, c["k"], dtype_name, name=f"{shape}/{dtype_name}")
+
+
+@pytest.mark.parametrize("k", [1, 2, 4, 8, 16, 32, 64, 128])
+def test_exact_k_sweep(cuda_dev, k):
+    print(f"case k-sweep k={k}", flush=True)
+    X, W, b = make_inputs(16, 128, 512, torch.bfloat16, seed=3, device=cuda_dev)
+    _run_check(X, W, b, k, "bf16", name=f"k={k}")
+
+
+@pytest.mark.parametrize("k", [1, 32, 64, 128])
+def test_exact_k_sweep_sampled(cuda_dev, k):
+    """F >= 16384 turns on the sampled threshold seed; every k through it."""
+    print(f"case k-sweep sampled k={k}", flush=True)
+    X, W, b = make_inputs(40, 256, 16384 + 37, torch.bfloat16, seed=4, device=cuda_dev)
+    _run_check(X, W, b, k, "bf16", name=f"sampled k={k}")
+
+
+@pytest.mark.parametrize("B", [1, 31, 33, 97, 130, 300])
+def test_exact_ragged_batch(cuda_dev, B):
+    print(f"case ragged B={B}", flush=True)
+    X, W, b = make_inputs(B, 128, 3000, torch.bfloat16, seed=5, device=cuda_dev)
+    _run_check(X, W, b, 16, "bf16", name=f"B={B}")
+
+
+def test_exact_k128_many_rows(cuda_dev):
+    """k=128 uses 64-row workgroups; B=200 spans several row chunks."""
+    X, W, b = make_inputs(200, 192, 20000, torch.bfloat16, seed=6, device=cuda_dev)
+    _run_check(X, W, b, 128, "bf16", name="k128 B200")
+
+
+def test_exact_ragged_d(cuda_dev):
+    """d not a multiple of 8: the op pads X and W_enc with zero columns."""
+    X, W, b = make_inputs(8, 100, 600, torch.bfloat16, seed=7, device=cuda_dev)
+    _run_check(X, W, b, 16, "bf16", name="d=100")
+    X, W, b = make_inputs(8, 30, 600, torch.float32, seed=7, device=cuda_dev)
+    _run_check(X, W, b, 8, "fp32", name="d=30 fp32")
+
+
+def test_edge_k_equals_F(cuda_dev):
+    X, W, b = make_inputs(4, 64, 16, torch.float32, seed=8, device=cuda_dev)
+    V, I = _run_check(X, W, b, 16, "fp32", name="k=F")
+    for i in range(4):
+        assert sorted(I[i].tolist()) == list(range(16))
+
+
+def test_edge_k_equals_1(cuda_dev):
+    X, W, b = make_inputs(8, 64, 256, torch.bfloat16, seed=9, device=cuda_dev)
+    V, I = _run_check(X, W, b, 1, "bf16", name="k=1")
+    S = _oracle_scores(X, W, b)
+    assert np.array_equal(I.cpu().numpy()[:, 0], np.argmax(S, axis=1))
+
+
+def test_edge_F_not_multiple_of_tile(cuda_dev):
+    X, W, b = make_inputs(8, 128, 300, torch.bfloat16, seed=10, device=cuda_dev)
+    _run_check(X, W, b, 16, "bf16", name="F=300")
+
+
+def test_edge_all_zero_X(cuda_dev):
+    """Scores are exactly b: the result is the top-k of b, bit for bit."""
+    for F in (128, 20011):
+        X = torch.zeros(4, 64, dtype=torch.bfloat16, device=cuda_dev)
+        _, W, b = make_inputs(4, 64, F, torch.bfloat16, seed=11, device=cuda_dev)
+        V, I = topk_sae_cuda_exact(X, W, b, 8)
+        bv = b.cpu().numpy()
+        order = np.lexsort((np.arange(F), -bv.astype(np.float64)))[:8]
+        for i in range(4):
+            assert np.array_equal(I[i].cpu().numpy(), order)
+            assert np.array_equal(V[i].cpu().numpy(), bv[order])
+
+
+def test_edge_large_bias(cuda_dev):
+    """One bias entry at +1e4 must be rank 0 in every row."""
+    X, W, b = make_inputs(16, 64, 20000, torch.bfloat16, seed=12, device=cuda_dev)
+    b[12345] = 1e4
+    V, I = _run_check(X, W, b, 8, "bf16", name="bias 1e4")
+    assert torch.all(I[:, 0] == 12345)
+
+
+def test_edge_batch_zero(cuda_dev):
+    X, W, b = make_inputs(1, 64, 256, torch.bfloat16, seed=13, device=cuda_dev)
+    V, I = topk_sae_cuda_exact(X[:0], W, b, 8)
+    assert V.shape == (0, 8) and I.shape == (0, 8)
+
+
+@pytest.mark.parametrize("F", [8000, 20480])
+def test_increasing_scores_adversarial(cuda_dev, F):
+    """Scores increase along F, so every later latent beats the running
+    threshold: exercises the queue-compaction path on every tile (F=8000 has
+    no sampled seed; F=20480 does)."""
+    B, d, k = 8, 64, 64
+    X = torch.ones(B, d, dtype=torch.float32, device=cuda_dev)
+    W = torch.zeros(F, d, dtype=torch.float32, device=cuda_dev)
+    b = torch.arange(F, dtype=torch.float32, device=cuda_dev) * 1e-3
+    _run_check(X, W, b, k, "fp32", name="increasing")
+    V, I = topk_sae_cuda_exact(X, W, b, k)
+    assert np.array_equal(I[0].cpu().numpy(), np.arange(F - 1, F - 1 - k, -1))
+
+
+def test_exact_ties_lower_index_first(cuda_dev):
+    """All scores equal: the k lowest indices, in order."""
+    X = torch.zeros(3, 64, dtype=torch.bfloat16, device=cuda_dev)
+    W = torch.zeros(5000, 64, dtype=torch.bfloat16, device=cuda_dev)
+    b = torch.full((5000,), 0.5, dtype=torch.float32, device=cuda_dev)
+    V, I = topk_sae_cuda_exact(X, W, b, 32)
+    assert torch.all(I == torch.arange(32, device=cuda_dev, dtype=torch.int32))
+    assert torch.all(V == 0.5)
+
+
+def test_torch_f64_scores_match_oracle(cuda_dev):
+    X, W, b = make_inputs(16, 256, 2048, torch.bfloat16, seed=14, device=cuda_dev)
+    S1 = _oracle_scores(X, W, b)
+    S2 = _gpu_scores_f64(X, W, b)
+    assert np.max(np.abs(S1 - S2)) < 1e-9
+
+
+@pytest.mark.parametrize("dtype_name", ["bf16", "fp16", "fp32"])
+def test_exact_config1_shape(cuda_dev, dtype_name):
+    """BASELINE config 1 shape (B=128 d=768 F=65536 k=32)."""
+    print(f"case config1 {dtype_name}", flush=True)
+    X, W, b = make_inputs(128, 768, 65536, DT[dtype_name], seed=0, device=cuda_dev)
+    _run_check(X, W, b, 32, dtype_name, scores="torch64", name=f"config1/{dtype_name}")
+
+
+def test_exact_deterministic(cuda_dev):
+    X, W, b = make_inputs(64, 512, 40000, torch.bfloat16, seed=15, device=cuda_dev)
+    V1, I1 = topk_sae_cuda_exact(X, W, b, 64)
+    V2, I2 = topk_sae_cuda_exact(X, W, b, 64)
+    assert torch.equal(V1, V2) and torch.equal(I1, I2)
+
+
+@pytest.mark.parametrize("dtype_name", ["fp32", "fp16", "bf16"])
+def test_exact_known_answers(cuda_dev, dtype_name):
+    """Scores exact in every dtype: values bit-exact and indices identical,
+    lower index first among equal scores (tests/golden/make_golden.py)."""
+    from golden.make_golden import load as load_golden
+    for X, W, b, k, Vk, Ik in load_golden():
+        Xt = torch.from_numpy(X).to(cuda_dev).to(DT[dtype_name])
+        Wt = torch.from_numpy(W).to(cuda_dev).to(DT[dtype_name])
+        bt = torch.from_numpy(b).to(cuda_dev)
+        V, I = topk_sae_cuda_exact(Xt, Wt, bt, k)
+        assert np.array_equal(V.cpu().numpy(), Vk), f"{dtype_name} {X.shape} {W.shape} k={k}"
+        assert np.array_equal(I.cpu().numpy(), Ik), f"{dtype_name} {X.shape} {W.shape} k={k}"
