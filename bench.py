@@ -1,0 +1,197 @@
+#!/usr/bin/env python3
+"""Benchmark of the streaming fused top-k SAE encoder on one MI355X.
+
+Default workload (the headline): exact encode, bf16 X and
+W_enc, fp32 b_enc, B=128, d=2048, F=262144, k=64.  One step = one call of
+topk_sae_cuda_exact over the resident batch.  Prints ONE JSON line.
+
+  python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
+
+Workloads: c2_bf16 (default), c2_fp16, c2_fp32, c1_bf16, c3_approx_c{16,32,64,128},
+c4_bf16, c4_bf16_heavy.  Only --gpus 1 is supported (one GPU per box).
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(ROOT, "streamtopk-sae_amd")
+for _p in (PKG_DIR, ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "fp16": 2500.0, "fp32": 157.3}
+METRIC = "rows/s + % of HBM-or-MFMA roofline, bf16 exact B=128 d=2048 F=262144 k=64"
+
+WORKLOADS = {
+    "c1_bf16": dict(B=128, d=768, F=65536, k=32, dtype="bf16", op="exact", label="BASELINE config 1"),
+    "c2_bf16": dict(B=128, d=2048, F=262144, k=64, dtype="bf16", op="exact", label="BASELINE config 2 (headline)"),
+    "c2_fp16": dict(B=128, d=2048, F=262144, k=64, dtype="fp16", op="exact", label="BASELINE config 2, fp16"),
+    "c2_fp32": dict(B=128, d=2048, F=262144, k=64, dtype="fp32", op="exact", label="BASELINE config 2, fp32"),
+    "c4_bf16": dict(B=1024, d=4096, F=262144, k=128, dtype="bf16", op="exact", label="BASELINE config 4"),
+    "c4_bf16_heavy": dict(B=1024, d=4096, F=262144, k=128, dtype="bf16", op="exact", heavy=True,
+                          label="BASELINE config 4, heavy-tailed W_enc"),
+}
+for _c in (16, 32, 64, 128):
+    WORKLOADS[f"c3_approx_c{_c}"] = dict(B=128, d=2048, F=1048576, k=32, c=_c, dtype="bf16", op="approx",
+                                         label=f"BASELINE config 3, c={_c}")
+
+
+def _cpu_cores():
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def cpu_baseline(X, W, b, k, seconds):
+    """Times the oracle's restatement of the reference CPU kernel (OpenMP over
+    rows, each row streaming all of W) on the first rows of the same batch."""
+    import numpy as np
+    import oracle
+    cores = _cpu_cores()
+    Xf = X.float().cpu().numpy()
+    Wf = W.float().cpu().numpy()
+    bf = b.float().cpu().numpy()
+    rows = min(cores, Xf.shape[0])
+    t0 = time.perf_counter()
+    oracle.cpu_stream(Xf[:rows], Wf, bf, k, nthreads=cores)
+    t1 = time.perf_counter() - t0
+    reps = max(1, int(seconds / max(t1, 1e-3)))
+    rows2 = min(Xf.shape[0], rows * reps)
+    if rows2 > rows:
+        t0 = time.perf_counter()
+        oracle.cpu_stream(Xf[:rows2], Wf, bf, k, nthreads=cores)
+        t1 = time.perf_counter() - t0
+        rows = rows2
+    return {"value": rows / t1, "unit": "rows/s", "cores": cores, "kind": "port",
+            "sample": f"rows 0..{rows - 1} of the same batch, full F and d, fp32 upcast inputs; "
+                      f"oracle/stk_oracle_cpu.c (reference streamtopk_cpu.cpp restated), {t1:.2f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="c2_bf16", choices=sorted(WORKLOADS))
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "the encoder would shard F across GPUs with one small all-gather of (B, k) candidates, "
+              "which is not built here.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from streamtopk_sae import _lib, make_inputs, topk_sae_cuda_approx, topk_sae_cuda_exact
+
+    wl = WORKLOADS[args.workload]
+    B, d, F, k, dtn = wl["B"], wl["d"], wl["F"], wl["k"], wl["dtype"]
+    dtype = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[dtn]
+    es = 4 if dtn == "fp32" else 2
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    X, W, b = make_inputs(B, d, F, dtype, seed=args.seed, device=dev, heavy_tail=wl.get("heavy", False))
+    torch.cuda.synchronize()
+    lib = _lib.load()
+
+    if wl["op"] == "exact":
+        def step():
+            return topk_sae_cuda_exact(X, W, b, k)
+        main_name = "main_kernel"
+    else:
+        c = wl["c"]
+
+        def step():
+            return topk_sae_cuda_approx(X, W, b, k, c)
+        main_name = "main_kernel"
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    base_mem = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+
+    _lib.check(lib.stk_profile_enable(1))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        V, I = step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    peak_extra = torch.cuda.max_memory_allocated() - base_mem
+
+    kern = {}
+    for name in ("sample_kernel", "seed_kernel", "main_kernel", "merge_kernel"):
+        tot = ctypes.c_double(0)
+        n = ctypes.c_int64(0)
+        _lib.check(lib.stk_profile_read(name.encode(), ctypes.byref(tot), ctypes.byref(n)))
+        if n.value:
+            kern[name] = {"avg_us": 1e3 * tot.value / n.value, "launches": n.value}
+    _lib.check(lib.stk_profile_enable(0))
+
+    ms_per_step = 1e3 * wall / args.steps
+    rows_per_s = B * args.steps / wall
+    w_bytes = F * d * es
+    alg_main = w_bytes + B * d * es + 4 * F                 # W + X + b streamed by main_kernel
+    alg_total = alg_main + 8 * B * k                        # + V, I (bench/run_bandwidth.py:73-77)
+    flops = 2.0 * B * d * F
+    main_us = kern[main_name]["avg_us"]
+    bw_main = alg_main / (main_us * 1e-6) / 1e9
+    tflops_main = flops / (main_us * 1e-6) / 1e12
+    ai = flops / alg_total
+    ridge = MFMA_PEAK_TFLOPS[dtn] * 1e12 / (HBM_PEAK_GBS * 1e9)
+    if ai < ridge:
+        roof = {"bound": "hbm", "achieved": round(bw_main, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(bw_main / HBM_PEAK_GBS, 4)}
+    else:
+        roof = {"bound": "mfma", "achieved": round(tflops_main, 2), "peak": MFMA_PEAK_TFLOPS[dtn],
+                "unit": "TFLOP/s", "frac": round(tflops_main / MFMA_PEAK_TFLOPS[dtn], 4)}
+    roof["kernel"] = main_name
+    roof["traffic"] = None
+    roof["alg_bytes_per_launch"] = alg_main
+    roof["avg_launch_us"] = round(main_us, 2)
+
+    out = {
+        "metric": METRIC if args.workload == "c2_bf16" else f"rows/s, {wl['label']}",
+        "value": round(rows_per_s, 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtn,
+        "data": f"synthetic: X~N(0,1), W_enc rows N(0,1/d) then L2-normalised, b_enc~N(0,0.1^2); seed {args.seed}",
+        "config": {"workload": f"{args.workload}: {wl['label']}", "op": wl["op"], "B": B, "d": d, "F": F,
+                   "k": k, **({"c": wl["c"]} if "c" in wl else {})},
+        "roofline": roof,
+        "pipeline": {"W_GBps_effective": round(w_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+                     "alg_bytes_per_step": alg_total,
+                     "hbm_frac_per_step": round(alg_total / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "tflops_per_step": round(flops / (ms_per_step * 1e-3) / 1e12, 2),
+                     "kernels": {n: round(v["avg_us"], 2) for n, v in kern.items()}},
+        "memory": {"peak_extra_bytes": int(peak_extra), "BxF_fp32_bytes": B * F * 4},
+        "reference_published": "A5000: ~60 rows/s on this config read off results/report/roofline.png "
+                               "(not tabulated; BASELINE.json published is empty)",
+    }
+    if not args.no_cpu and wl["op"] == "exact":
+        out["cpu_baseline"] = cpu_baseline(X, W, b, k, args.cpu_seconds)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

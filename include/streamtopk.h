@@ -58,7 +58,8 @@ int stk_exact_workspace_bytes(int64_t B, int64_t d, int64_t F, int64_t k, int dt
  * Replaces streamtopk_cuda_exact_forward (streamtopk_exact.cu:788-833),
  * bound in the reference at bindings.cpp:33 and called from ops.py:57.
  * k must be one of 1,2,4,8,16,32,64,128 and <= F; d <= 4096; d must be a
- * multiple of 8 (fp16/bf16) or 4 (fp32). */
+ * multiple of 64 (fp16/bf16) or 32 (fp32): one 128-byte d-step of a row (the
+ * Python op zero-pads other d). */
 int stk_exact_forward(const void* X, const void* W, const float* b, float* V, int32_t* I,
                       int64_t B, int64_t d, int64_t F, int64_t k, int dtype,
                       void* workspace, size_t workspace_bytes, void* stream);
@@ -87,6 +88,18 @@ int stk_approx_forward(const void* X, const void* W, const float* b, float* V, i
  * rows in heap order, topk_buffer.hpp:9). */
 int stk_cpu_forward(const float* X, const float* W, const float* b, float* V, int32_t* I,
                     int64_t B, int64_t d, int64_t F, int64_t k, int num_threads);
+
+/* Per-kernel timing (no counterpart in the reference; used by bench.py).
+ * While enabled, every device entry point called on this thread records a HIP
+ * event pair on its stream around each kernel it launches.  Enabling (on=1)
+ * discards earlier records; on=0 stops recording and frees the events. */
+int stk_profile_enable(int on);
+
+/* Total milliseconds and number of launches recorded for `kernel`
+ * ("sample_kernel", "seed_kernel", "main_kernel", "merge_kernel",
+ * "group_kernel", "cand_kernel") since stk_profile_enable(1).  Waits for the
+ * recorded events to complete. */
+int stk_profile_read(const char* kernel, double* total_ms, int64_t* launches);
 
 #ifdef __cplusplus
 }

@@ -6,6 +6,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "../../include/streamtopk.h"
 #include "stk_internal.h"
@@ -36,6 +37,50 @@ bool k_supported(int64_t k)
 static int hip_fail(hipError_t e, const char* what)
 {
     return set_error(STK_E_HIP, "%s failed: %s", what, hipGetErrorString(e));
+}
+
+// ---------------------------------------------------------------------------
+// Optional per-kernel event timing (stk_profile_enable / stk_profile_read).
+// ---------------------------------------------------------------------------
+struct ProfRec {
+    const char* name;
+    hipEvent_t a, b;
+};
+static thread_local bool g_prof = false;
+static thread_local std::vector<ProfRec> g_recs;
+static thread_local std::vector<hipEvent_t> g_pool;
+
+static hipEvent_t prof_event()
+{
+    if (!g_pool.empty()) {
+        hipEvent_t e = g_pool.back();
+        g_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+static int prof_begin(const char* name, hipStream_t st)
+{
+    if (!g_prof) return -1;
+    ProfRec r{name, prof_event(), prof_event()};
+    if (!r.a || !r.b) return -1;
+    (void)hipEventRecord(r.a, st);
+    g_recs.push_back(r);
+    return (int)g_recs.size() - 1;
+}
+
+static void prof_end(int idx, hipStream_t st)
+{
+    if (idx >= 0 && idx < (int)g_recs.size()) (void)hipEventRecord(g_recs[idx].b, st);
+}
+
+static void prof_release()
+{
+    for (auto& r : g_recs) { g_pool.push_back(r.a); g_pool.push_back(r.b); }
+    g_recs.clear();
 }
 
 // Compute units of the current device (queried once per device).
@@ -69,17 +114,14 @@ struct ExactPlan {
     bool sample;
     int64_t samp_count;
     int samp_log2;
-    int sNB;
-    int64_t s_nbc, s_gx, spp;
-    int nsplit;
     size_t off_seed, off_thr, off_P, off_keys, off_cnt, total;
 };
 
 static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int dtype, int ncu)
 {
     ExactPlan p;
-    const int64_t DS = (dtype == STK_DTYPE_F32) ? 32 : 64;
-    const int64_t nds = cdiv(d, DS);
+    (void)d;
+    (void)dtype;
     const int64_t bblocks = cdiv(B > 0 ? B : 1, 32);
     const int64_t nb_max = (k > 64) ? 2 : 4;   // k=128 queues need the LDS of 64 rows
     p.NB = (int)(bblocks < nb_max ? bblocks : nb_max);
@@ -97,24 +139,13 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
     p.sample = F >= kSampleMinF;
     p.samp_count = 0;
     p.samp_log2 = 0;
-    p.sNB = p.NB;
-    p.s_nbc = p.s_gx = p.spp = 0;
-    p.nsplit = 0;
     if (p.sample) {
+        // every (1 << samp_log2)-th latent, at most kSampleTarget of them
         int l = ilog2_floor(F / kSampleTarget);
         if (l < 4) l = 4;
         p.samp_log2 = l;
         p.samp_count = F >> l;
         if (p.samp_count > kSampleTarget) p.samp_count = kSampleTarget;
-        p.sNB = (int)(bblocks < 4 ? bblocks : 4);
-        if (p.sNB == 3) p.sNB = 4;
-        p.s_nbc = cdiv(B, 32 * p.sNB);
-        p.s_gx = cdiv(p.samp_count, 128);
-        int64_t ns = ncu / (p.s_gx * p.s_nbc);
-        if (ns < 1) ns = 1;
-        if (ns > nds) ns = nds;
-        p.spp = cdiv(nds, ns);
-        p.nsplit = (int)cdiv(nds, p.spp);
     }
     size_t off = 0;
     p.off_seed = off;
@@ -122,7 +153,7 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
     p.off_thr = off;
     if (p.sample) off = align256(off + (size_t)B * 8);
     p.off_P = off;
-    if (p.sample) off = align256(off + (size_t)p.nsplit * B * p.samp_count * 4);
+    if (p.sample) off = align256(off + (size_t)B * p.samp_count * 4);
     p.off_keys = off;
     off = align256(off + (size_t)B * p.nwg * p.cap * 8);
     p.off_cnt = off;
@@ -143,7 +174,8 @@ static int check_shape_common(int64_t B, int64_t d, int64_t F, int dtype)
     if (B < 0 || d < 1 || F < 1) return set_error(STK_E_INVALID, "invalid shape: B=%lld d=%lld F=%lld",
                                                   (long long)B, (long long)d, (long long)F);
     if (F > 0x7FFFFFFELL) return set_error(STK_E_INVALID, "F=%lld exceeds the int32 index range", (long long)F);
-    const int64_t q = (dtype == STK_DTYPE_F32) ? 4 : 8;
+    // one d-step is 128 bytes of a row: 64 fp16/bf16 or 32 fp32 elements
+    const int64_t q = (dtype == STK_DTYPE_F32) ? 32 : 64;
     if (d % q)
         return set_error(STK_E_INVALID,
                          "d=%lld must be a multiple of %lld for %s inputs (pad X and W_enc with zero columns)",
@@ -182,17 +214,20 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     uint64_t* thr = (uint64_t*)(ws + p.off_thr);
     if (p.sample) {
         SampleArgs sa;
-        sa.X = X; sa.W = W; sa.B = B; sa.d = d;
+        sa.X = X; sa.W = W; sa.bias = b; sa.B = B; sa.d = d;
         sa.count = p.samp_count; sa.samp_log2 = p.samp_log2;
-        sa.steps_per_split = p.spp;
         sa.P = (float*)(ws + p.off_P);
-        e = launch_sample(dt, p.sNB, sa, dim3((unsigned)p.s_gx, (unsigned)p.nsplit, (unsigned)p.s_nbc), st);
+        int pi = prof_begin("sample_kernel", st);
+        e = launch_sample(dt, sa, dim3((unsigned)cdiv(p.samp_count, 32), (unsigned)cdiv(B, 32)), st);
+        prof_end(pi, st);
         if (e != hipSuccess) return hip_fail(e, "sample_kernel launch");
         SeedArgs sd;
-        sd.P = sa.P; sd.bias = b; sd.B = B; sd.count = p.samp_count;
-        sd.nsplit = p.nsplit; sd.samp_log2 = p.samp_log2; sd.k = (int)k;
+        sd.P = sa.P; sd.count = p.samp_count;
+        sd.samp_log2 = p.samp_log2; sd.k = (int)k;
         sd.seed_keys = seed; sd.thr = thr;
+        pi = prof_begin("seed_kernel", st);
         e = launch_seed(sd, B, st);
+        prof_end(pi, st);
         if (e != hipSuccess) return hip_fail(e, "seed_kernel launch");
     }
     MainArgs ma;
@@ -204,14 +239,18 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     ma.samp_log2 = p.samp_log2;
     ma.out_keys = (uint64_t*)(ws + p.off_keys);
     ma.out_cnt = (int32_t*)(ws + p.off_cnt);
+    int pm = prof_begin("main_kernel", st);
     e = launch_main(dt, p.NB, ma, dim3((unsigned)p.nwg, (unsigned)p.nbc), st);
+    prof_end(pm, st);
     if (e != hipSuccess) return hip_fail(e, "main_kernel launch");
     MergeArgs mg;
     mg.seed_keys = p.sample ? seed : nullptr;
     mg.seg_keys = ma.out_keys; mg.seg_cnt = ma.out_cnt;
     mg.nseg = p.nwg; mg.cap = p.cap; mg.k = (int)k;
     mg.V = V; mg.I = I;
+    pm = prof_begin("merge_kernel", st);
     e = launch_merge(mg, B, st);
+    prof_end(pm, st);
     if (e != hipSuccess) return hip_fail(e, "merge_kernel launch");
     return 0;
 }
@@ -343,13 +382,50 @@ int stk_approx_forward(const void* X, const void* W, const float* b, float* V, i
     ga.X = X; ga.W = W; ga.bias = b; ga.B = B; ga.d = d; ga.F = F; ga.c = (int)c;
     ga.num_groups = p.num_groups; ga.tiles_per_wg = p.tpw;
     ga.cand_vals = cand_vals; ga.cand_idxs = cand_idxs;
+    int pg = prof_begin("group_kernel", st);
     hipError_t e = launch_group(dtype, p.NB, ga, dim3((unsigned)p.nwg, (unsigned)p.nbc), st);
+    prof_end(pg, st);
     if (e != hipSuccess) return hip_fail(e, "group_kernel launch");
     CandArgs ca;
     ca.cand_vals = cand_vals; ca.cand_idxs = cand_idxs;
     ca.per_row = p.num_groups * c; ca.k = (int)k; ca.V = V; ca.I = I;
+    pg = prof_begin("cand_kernel", st);
     e = launch_cand(ca, B, st);
+    prof_end(pg, st);
     if (e != hipSuccess) return hip_fail(e, "cand_kernel launch");
+    return 0;
+}
+
+int stk_profile_enable(int on)
+{
+    clear_error();
+    prof_release();
+    g_prof = on != 0;
+    if (!g_prof) {
+        for (hipEvent_t e : g_pool) (void)hipEventDestroy(e);
+        g_pool.clear();
+    }
+    return 0;
+}
+
+int stk_profile_read(const char* kernel, double* total_ms, int64_t* launches)
+{
+    clear_error();
+    if (!kernel || !total_ms || !launches) return set_error(STK_E_INVALID, "null argument");
+    double tot = 0.0;
+    int64_t n = 0;
+    for (auto& r : g_recs) {
+        if (std::strcmp(r.name, kernel) != 0) continue;
+        hipError_t e = hipEventSynchronize(r.b);
+        if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+        float ms = 0.f;
+        e = hipEventElapsedTime(&ms, r.a, r.b);
+        if (e != hipSuccess) return hip_fail(e, "hipEventElapsedTime");
+        tot += ms;
+        ++n;
+    }
+    *total_ms = tot;
+    *launches = n;
     return 0;
 }
 

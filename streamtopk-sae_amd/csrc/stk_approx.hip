@@ -53,7 +53,7 @@ __global__ __launch_bounds__(kThreads, 1) void group_kernel(GroupArgs a)
     const int64_t t1 = (t0 + a.tiles_per_wg < num_tiles) ? t0 + a.tiles_per_wg : num_tiles;
 
     for (int64_t tile = t0; tile < t1; ++tile) {
-        const int64_t fw0 = tile * kTileLatents + wave * 64;
+        const int64_t fw0 = tile * kGroupTile + wave * 64;
 #pragma unroll
         for (int fa = 0; fa < FRAGS; ++fa) {
             int64_t f = fw0 + fa * 32 + jl;
@@ -86,7 +86,7 @@ __global__ __launch_bounds__(kThreads, 1) void group_kernel(GroupArgs a)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int lt = wave * 64 + fa * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-                    const int64_t f = tile * kTileLatents + lt;
+                    const int64_t f = tile * kGroupTile + lt;
                     const int g = lt / G, p = lt % G;
                     keys[((size_t)g * 32 + jl) * G + p] =
                         (f < F) ? make_key(acc[fa][n][r] + bias_r[fa][r], f) : 0ull;

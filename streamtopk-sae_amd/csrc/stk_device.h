@@ -174,33 +174,224 @@ struct MainLoop {
             }
     }
 
+    // One d-step of the pipeline: publish X(s+1) to LDS, multiply step s,
+    // refill this step's register sets with step s+4, barrier.  Loads are
+    // issued X-then-W per step, so waiting for X(s+1) (issued three steps ago)
+    // leaves the W loads of steps s+2..s+4 in flight.
+#define STK_PIPE_STEP(J, JN, XSC, XSN)                                          \
+    do {                                                                       \
+        const int64_t s = s_begin + base + (J);                               \
+        if (s < s_end) {                                                       \
+            if (s + 1 < s_end) store_x(x##JN, XSN, tid);                      \
+            compute(acc, w##J, XSC);                                           \
+            if (s + 4 < s_end) {                                               \
+                load_x(x##J, s + 4, tid);                                      \
+                load_w(w##J, s + 4);                                           \
+            }                                                                  \
+            __syncthreads();                                                   \
+        }                                                                      \
+    } while (0)
+
     __device__ __forceinline__ void run(f32x16 (&acc)[FRAGS][NB], int64_t s_begin, int64_t s_end,
                                         unsigned char* xs0, unsigned char* xs1, int tid) const
     {
         if (s_begin >= s_end) return;
-        u32x4 wA[FRAGS][4], wB[FRAGS][4];
-        u32x4 xr[kXChunks];
-        load_w(wA, s_begin);
-        load_x(xr, s_begin, tid);
-        store_x(xr, xs0, tid);
-        if (s_begin + 1 < s_end) {
-            load_w(wB, s_begin + 1);
-            load_x(xr, s_begin + 1, tid);
-        }
+        u32x4 w0[FRAGS][4], w1[FRAGS][4], w2[FRAGS][4], w3[FRAGS][4];
+        u32x4 x0[kXChunks], x1[kXChunks], x2[kXChunks], x3[kXChunks];
+        load_x(x0, s_begin, tid);
+        load_w(w0, s_begin);
+        if (s_begin + 1 < s_end) { load_x(x1, s_begin + 1, tid); load_w(w1, s_begin + 1); }
+        if (s_begin + 2 < s_end) { load_x(x2, s_begin + 2, tid); load_w(w2, s_begin + 2); }
+        if (s_begin + 3 < s_end) { load_x(x3, s_begin + 3, tid); load_w(w3, s_begin + 3); }
+        store_x(x0, xs0, tid);
         __syncthreads();
-        for (int64_t s = s_begin; s < s_end; s += 2) {
-            if (s + 1 < s_end) store_x(xr, xs1, tid);
-            if (s + 2 < s_end) load_x(xr, s + 2, tid);
-            compute(acc, wA, xs0);
-            if (s + 2 < s_end) load_w(wA, s + 2);
-            __syncthreads();
-            if (s + 1 < s_end) {
-                if (s + 2 < s_end) store_x(xr, xs0, tid);
-                if (s + 3 < s_end) load_x(xr, s + 3, tid);
-                compute(acc, wB, xs1);
-                if (s + 3 < s_end) load_w(wB, s + 3);
+        for (int64_t base = 0; s_begin + base < s_end; base += 4) {
+            STK_PIPE_STEP(0, 1, xs0, xs1);
+            STK_PIPE_STEP(1, 2, xs1, xs0);
+            STK_PIPE_STEP(2, 3, xs0, xs1);
+            STK_PIPE_STEP(3, 0, xs1, xs0);
+        }
+    }
+#undef STK_PIPE_STEP
+};
+
+// ---------------------------------------------------------------------------
+// TileStream: the score main loop as one flat stream of d-steps over all the
+// tiles a workgroup owns.  A tile is 32*FRAGS*WAVES latents x 32*NB rows and
+// takes nds4 d-steps: the nds = d / DS real ones (d is a multiple of the
+// d-step) rounded up to a multiple of 4; the padding steps load a valid step
+// again and skip their MFMAs.  Four register sets of W (and of X) keep the
+// loads of the next three d-steps in flight -- across tile boundaries too.
+// Every load is unconditional (rows past F or B and steps past the end are
+// clamped to valid addresses; the scores they produce are never selected), so
+// the in-order vmcnt waits never drain the prefetched W loads.  X is staged
+// through two LDS buffers (one barrier per d-step).
+//
+// run() calls epi(t, acc, bias) after the last d-step of tile t (0-based
+// within the workgroup's tiles) and then clears acc.  The epilogue may use LDS
+// other than the two X buffers and must not issue global loads (waiting for
+// one would also wait for every older prefetched W load); the bias of tile t
+// it receives was loaded during the previous tile.
+// ---------------------------------------------------------------------------
+template <int DT, int NB, int FRAGS, int WAVES>
+struct TileStream {
+    static constexpr int DS = Dt<DT>::DS;
+    static constexpr int ES = Dt<DT>::esize;
+    static constexpr int kThr = 64 * WAVES;
+    static constexpr int kXTotal = 32 * NB * 8;                    // 16-byte X chunks per d-step
+    static constexpr int kXChunks = (kXTotal + kThr - 1) / kThr;   // per thread
+    static constexpr int kTileF = 32 * FRAGS * WAVES;             // latents per tile
+    static_assert(kXTotal % kThr == 0 || kXChunks == 1, "X chunk split");
+
+    const float* bias;
+    int64_t F;
+    int64_t tile_begin;
+    int ntiles, nds, nds4;
+    int tid, lane, wave, h, jl;
+    const unsigned char* W;
+    int64_t w_row_bytes;
+
+    // load cursor (uniform) and per-lane row pointers of the cursor's tile
+    int lt, ls;
+    const unsigned char* lw[FRAGS];
+    const unsigned char* lx[kXChunks];
+    bool xok[kXChunks];
+
+    __device__ __forceinline__ void init_x(const unsigned char* X, int64_t B, int64_t b0, int64_t d)
+    {
+#pragma unroll
+        for (int p = 0; p < kXChunks; ++p) {
+            const int c = tid + kThr * p;
+            const int row = (c >> 3) % (32 * NB), c16 = c & 7;
+            int64_t r = b0 + row;
+            r = (r < B) ? r : B - 1;
+            lx[p] = X + (r * d) * ES + c16 * 16;
+            xok[p] = c < kXTotal;
+        }
+    }
+
+    __device__ __forceinline__ void set_rows(int t)
+    {
+        const int64_t tile = tile_begin + (t < ntiles ? t : ntiles - 1);
+#pragma unroll
+        for (int a = 0; a < FRAGS; ++a) {
+            int64_t f = tile * kTileF + wave * (32 * FRAGS) + a * 32 + jl;
+            f = (f < F) ? f : F - 1;
+            lw[a] = W + f * w_row_bytes + h * 64;
+        }
+    }
+
+    __device__ __forceinline__ void issue(u32x4 (&xr)[kXChunks], u32x4 (&w)[FRAGS][4])
+    {
+        const int s = (lt >= ntiles || ls >= nds) ? nds - 1 : ls;
+        const int64_t so = (int64_t)s * kStepBytes;
+#pragma unroll
+        for (int p = 0; p < kXChunks; ++p) xr[p] = *(const u32x4*)(lx[p] + so);
+#pragma unroll
+        for (int a = 0; a < FRAGS; ++a) {
+            const unsigned char* pw = lw[a] + so;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) w[a][q] = *(const u32x4*)(pw + q * 16);
+        }
+        if (lt < ntiles && ++ls == nds4) {
+            ls = 0;
+            ++lt;
+            if (lt < ntiles) set_rows(lt);
+        }
+    }
+
+    __device__ __forceinline__ void store_x(const u32x4 (&xr)[kXChunks], unsigned char* xs) const
+    {
+#pragma unroll
+        for (int p = 0; p < kXChunks; ++p) {
+            const int c = tid + kThr * p;
+            const int row = c >> 3, c16 = c & 7;
+            if (kXTotal % kThr == 0 || xok[p]) *(u32x4*)(xs + row * kXRowStride + c16 * 16) = xr[p];
+        }
+    }
+
+    __device__ __forceinline__ void compute(f32x16 (&acc)[FRAGS][NB], const u32x4 (&w)[FRAGS][4],
+                                            const unsigned char* xs) const
+    {
+        u32x4 bx[NB][4];
+#pragma unroll
+        for (int n = 0; n < NB; ++n)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                bx[n][q] = *(const u32x4*)(xs + (32 * n + jl) * kXRowStride + h * 64 + q * 16);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int n = 0; n < NB; ++n)
+#pragma unroll
+                for (int a = 0; a < FRAGS; ++a) mfma_quad<DT>(acc[a][n], w[a][q], bx[n][q]);
+    }
+
+    // Bias of this lane's latents of tile t: entry [a][r] is latent
+    // tile*kTileF + wave*32*FRAGS + a*32 + 8*(r/4) + 4*h + r%4 (0 past F).
+    __device__ __forceinline__ void tile_bias(float (&bv)[FRAGS][16], int t) const
+    {
+        const int64_t fw0 = (tile_begin + t) * kTileF + wave * (32 * FRAGS);
+#pragma unroll
+        for (int a = 0; a < FRAGS; ++a)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t f = fw0 + a * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+                bv[a][r] = bias[(f < F) ? f : F - 1];
+            }
+    }
+
+    template <class Epi>
+    __device__ __forceinline__ void run(f32x16 (&acc)[FRAGS][NB], unsigned char* xs0, unsigned char* xs1,
+                                        Epi epi)
+    {
+        if (ntiles <= 0) return;
+        lt = 0;
+        ls = 0;
+        set_rows(0);
+        u32x4 w0[FRAGS][4], w1[FRAGS][4], w2[FRAGS][4], w3[FRAGS][4];
+        u32x4 x0[kXChunks], x1[kXChunks], x2[kXChunks], x3[kXChunks];
+        float bv[FRAGS][16];
+        tile_bias(bv, 0);
+        issue(x0, w0);
+        issue(x1, w1);
+        issue(x2, w2);
+        issue(x3, w3);
+        store_x(x0, xs0);
+#pragma unroll
+        for (int a = 0; a < FRAGS; ++a)
+#pragma unroll
+            for (int n = 0; n < NB; ++n)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[a][n][r] = 0.f;
+        __syncthreads();
+        for (int t = 0; t < ntiles; ++t) {
+            for (int s = 0; s < nds4; s += 4) {
+                store_x(x1, xs1);
+                if (s < nds) compute(acc, w0, xs0);
+                issue(x0, w0);
+                __syncthreads();
+                store_x(x2, xs0);
+                if (s + 1 < nds) compute(acc, w1, xs1);
+                issue(x1, w1);
+                __syncthreads();
+                store_x(x3, xs1);
+                if (s + 2 < nds) compute(acc, w2, xs0);
+                issue(x2, w2);
+                __syncthreads();
+                store_x(x0, xs0);
+                if (s + 3 < nds) compute(acc, w3, xs1);
+                issue(x3, w3);
                 __syncthreads();
             }
+            epi(t, acc, bv);
+            if (t + 1 < ntiles) tile_bias(bv, t + 1);
+#pragma unroll
+            for (int a = 0; a < FRAGS; ++a)
+#pragma unroll
+                for (int n = 0; n < NB; ++n)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[a][n][r] = 0.f;
         }
     }
 };

@@ -5,8 +5,11 @@
 
 namespace stk {
 
-constexpr int kTileLatents = 256;    // latents per main_kernel tile (4 waves x 64)
+constexpr int kMainWaves = 4;        // wavefronts per main_kernel workgroup (1 per SIMD)
+constexpr int kMainThreads = 64 * kMainWaves;
+constexpr int kTileLatents = 32 * kMainWaves;   // latents per main_kernel tile
 constexpr int kApproxGroup = 128;    // latent group of the approximate variant
+constexpr int kGroupTile = 256;      // latents per group_kernel tile (two groups)
 constexpr int kSampleTarget = 4096;  // sampled latents that seed the thresholds
 constexpr int64_t kSampleMinF = 16384;
 
@@ -28,18 +31,17 @@ struct MainArgs {
 struct SampleArgs {
     const void* X;
     const void* W;
+    const float* bias;
     int64_t B, d;
     int64_t count;
     int samp_log2;
-    int64_t steps_per_split;
-    float* P;                    // [nsplit][B][count]
+    float* P;                    // [B][count] scores of the sampled latents
 };
 
 struct SeedArgs {
     const float* P;
-    const float* bias;
-    int64_t B, count;
-    int nsplit, samp_log2, k;
+    int64_t count;
+    int samp_log2, k;
     uint64_t* seed_keys;         // [B][k], descending
     uint64_t* thr;               // [B]
 };
@@ -78,7 +80,7 @@ size_t main_lds_bytes(int NB, int cap);
 size_t group_lds_bytes(int NB);
 
 hipError_t launch_main(int dt, int NB, const MainArgs& a, dim3 grid, hipStream_t st);
-hipError_t launch_sample(int dt, int NB, const SampleArgs& a, dim3 grid, hipStream_t st);
+hipError_t launch_sample(int dt, const SampleArgs& a, dim3 grid, hipStream_t st);
 hipError_t launch_seed(const SeedArgs& a, int64_t rows, hipStream_t st);
 hipError_t launch_merge(const MergeArgs& a, int64_t rows, hipStream_t st);
 hipError_t launch_group(int dt, int NB, const GroupArgs& a, dim3 grid, hipStream_t st);

@@ -23,11 +23,11 @@ namespace stk {
 // main_kernel
 // ---------------------------------------------------------------------------
 template <int DT, int NB>
-__global__ __launch_bounds__(kThreads, 1) void main_kernel(MainArgs a)
+__global__ __launch_bounds__(kMainThreads, 1) void main_kernel(MainArgs a)
 {
     constexpr int BT = 32 * NB;
-    constexpr int FRAGS = 2;
-    constexpr int ES = Dt<DT>::esize;
+    constexpr int FRAGS = 1;
+    constexpr int WAVES = kMainWaves;
     constexpr int DS = Dt<DT>::DS;
     extern __shared__ __align__(16) unsigned char smem[];
     unsigned char* xs0 = smem;
@@ -40,60 +40,47 @@ __global__ __launch_bounds__(kThreads, 1) void main_kernel(MainArgs a)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, jl = lane & 31;
     const int64_t b0 = (int64_t)blockIdx.y * BT;
-    const int64_t B = a.B, d = a.d, F = a.F;
+    const int64_t B = a.B, F = a.F;
     const int k = a.k;
 
-    for (int i = tid; i < BT; i += kThreads) {
+    for (int i = tid; i < BT; i += kMainThreads) {
         cnt[i] = 0;
         thr[i] = (a.thr0 != nullptr && b0 + i < B) ? a.thr0[b0 + i] : 0ull;
     }
-    __syncthreads();
 
-    MainLoop<DT, NB, FRAGS> ml;
-    ml.X = (const unsigned char*)a.X;
-    ml.B = B;
-    ml.d = d;
-    ml.b0 = b0;
-    ml.lane = lane;
-    ml.h = h;
-    const int64_t nds = (d + DS - 1) / DS;
-    const unsigned char* W = (const unsigned char*)a.W;
+    TileStream<DT, NB, FRAGS, WAVES> ts;
+    ts.W = (const unsigned char*)a.W;
+    ts.w_row_bytes = a.d * Dt<DT>::esize;
+    ts.bias = a.bias;
+    ts.F = F;
+    ts.tile_begin = (int64_t)blockIdx.x * a.tiles_per_wg;
+    {
+        const int64_t t1 = ts.tile_begin + a.tiles_per_wg;
+        ts.ntiles = (int)((t1 < a.num_tiles ? t1 : a.num_tiles) - ts.tile_begin);
+    }
+    ts.nds = (int)(a.d / DS);
+    ts.nds4 = (ts.nds + 3) & ~3;
+    ts.tid = tid;
+    ts.lane = lane;
+    ts.wave = wave;
+    ts.h = h;
+    ts.jl = jl;
+    ts.init_x((const unsigned char*)a.X, B, b0, a.d);
     const int64_t smask = a.samp_count ? ((int64_t)1 << a.samp_log2) - 1 : 0;
 
-    const int64_t t0 = (int64_t)blockIdx.x * a.tiles_per_wg;
-    const int64_t t1 = (t0 + a.tiles_per_wg < a.num_tiles) ? t0 + a.tiles_per_wg : a.num_tiles;
-
-    for (int64_t tile = t0; tile < t1; ++tile) {
-        const int64_t fw0 = tile * kTileLatents + wave * 64;
-#pragma unroll
-        for (int fa = 0; fa < FRAGS; ++fa) {
-            int64_t f = fw0 + fa * 32 + jl;
-            f = (f < F) ? f : F - 1;
-            ml.wrow[fa] = W + f * d * ES + h * 64;
-        }
-        f32x16 acc[FRAGS][NB];
-#pragma unroll
-        for (int fa = 0; fa < FRAGS; ++fa)
-#pragma unroll
-            for (int n = 0; n < NB; ++n)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[fa][n][r] = 0.f;
-
-        ml.run(acc, 0, nds, xs0, xs1, tid);
-
-        // ---- epilogue: bias, filter against the row thresholds ----
-        float bias_r[FRAGS][16];
+    f32x16 acc[FRAGS][NB];
+    ts.run(acc, xs0, xs1, [&](int t, f32x16 (&ac)[FRAGS][NB], const float (&bias_r)[FRAGS][16]) {
+        // this lane's latent for accumulator register r
+        const int64_t fw0 = (ts.tile_begin + t) * kTileLatents + wave * 32 + h * 4;
+        // ---- filter against the row thresholds ----
         uint32_t vmask = 0;
 #pragma unroll
-        for (int fa = 0; fa < FRAGS; ++fa)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t f = fw0 + fa * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-                bool ok = f < F;
-                if (a.samp_count && (f & smask) == 0 && (f >> a.samp_log2) < a.samp_count) ok = false;
-                bias_r[fa][r] = a.bias[ok ? f : 0];
-                if (ok) vmask |= 1u << (fa * 16 + r);
-            }
+        for (int r = 0; r < 16; ++r) {
+            const int64_t f = fw0 + (r >> 2) * 8 + (r & 3);
+            bool ok = f < F;
+            if (a.samp_count && (f & smask) == 0 && (f >> a.samp_log2) < a.samp_count) ok = false;
+            if (ok) vmask |= 1u << r;
+        }
         uint32_t pend[NB];
         uint64_t thr_r[NB];
 #pragma unroll
@@ -105,16 +92,12 @@ __global__ __launch_bounds__(kThreads, 1) void main_kernel(MainArgs a)
                 const float tv = key_value(thr_r[n]);
                 const bool all = thr_r[n] == 0ull;
 #pragma unroll
-                for (int fa = 0; fa < FRAGS; ++fa)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const uint32_t bit = 1u << (fa * 16 + r);
-                        const float s = acc[fa][n][r] + bias_r[fa][r];
-                        if ((vmask & bit) && (all || !(s < tv))) {
-                            const int64_t f = fw0 + fa * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-                            if (make_key(s, f) > thr_r[n]) pend[n] |= bit;
-                        }
+                for (int r = 0; r < 16; ++r) {
+                    const float sc = ac[0][n][r] + bias_r[0][r];
+                    if ((vmask >> r & 1u) && (all || !(sc < tv))) {
+                        if (make_key(sc, fw0 + (r >> 2) * 8 + (r & 3)) > thr_r[n]) pend[n] |= 1u << r;
                     }
+                }
             }
         }
 
@@ -129,23 +112,19 @@ __global__ __launch_bounds__(kThreads, 1) void main_kernel(MainArgs a)
                 if (pend[n] == 0) continue;
                 const int j = 32 * n + jl;
 #pragma unroll
-                for (int fa = 0; fa < FRAGS; ++fa)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const uint32_t bit = 1u << (fa * 16 + r);
-                        if (pend[n] & bit) {
-                            const int64_t f = fw0 + fa * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-                            const uint64_t key = make_key(acc[fa][n][r] + bias_r[fa][r], f);
-                            const int pos = atomicAdd(&cnt[j], 1);
-                            if (pos < cap) {
-                                q[(size_t)j * cap + pos] = key;
-                                pend[n] &= ~bit;
-                            }
+                for (int r = 0; r < 16; ++r) {
+                    if (pend[n] >> r & 1u) {
+                        const uint64_t key = make_key(ac[0][n][r] + bias_r[0][r], fw0 + (r >> 2) * 8 + (r & 3));
+                        const int pos = atomicAdd(&cnt[j], 1);
+                        if (pos < cap) {
+                            q[(size_t)j * cap + pos] = key;
+                            pend[n] &= ~(1u << r);
                         }
                     }
+                }
             }
             __syncthreads();
-            for (int row = wave; row < BT; row += kWaves) {
+            for (int row = wave; row < BT; row += WAVES) {
                 if (cnt[row] >= cap) {
                     // wave-wide rank compaction of a full queue to its top-k
                     uint64_t* qr = q + (size_t)row * cap;
@@ -174,22 +153,19 @@ __global__ __launch_bounds__(kThreads, 1) void main_kernel(MainArgs a)
                 if (pend[n] == 0) continue;
                 thr_r[n] = thr[32 * n + jl];
 #pragma unroll
-                for (int fa = 0; fa < FRAGS; ++fa)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const uint32_t bit = 1u << (fa * 16 + r);
-                        if (pend[n] & bit) {
-                            const int64_t f = fw0 + fa * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-                            if (!(make_key(acc[fa][n][r] + bias_r[fa][r], f) > thr_r[n])) pend[n] &= ~bit;
-                        }
+                for (int r = 0; r < 16; ++r) {
+                    if (pend[n] >> r & 1u) {
+                        if (!(make_key(ac[0][n][r] + bias_r[0][r], fw0 + (r >> 2) * 8 + (r & 3)) > thr_r[n]))
+                            pend[n] &= ~(1u << r);
                     }
+                }
             }
         }
-    }
+    });
 
     // ---- emit this workgroup's queues ----
     __syncthreads();
-    for (int idx = tid; idx < BT * cap; idx += kThreads) {
+    for (int idx = tid; idx < BT * cap; idx += kMainThreads) {
         const int row = idx / cap, e = idx - row * cap;
         if (b0 + row < B) {
             const int c = cnt[row] < cap ? cnt[row] : cap;
@@ -201,51 +177,67 @@ __global__ __launch_bounds__(kThreads, 1) void main_kernel(MainArgs a)
 }
 
 // ---------------------------------------------------------------------------
-// sample_kernel: P[split][row][i] = sum over the split's d-steps of
-// X[row] . W[i * stride]   (no bias; seed_kernel adds it after summing splits)
+// sample_kernel: P[row][i] = X[row] . W[i << samp_log2] + b[i << samp_log2]
+// for the sampled latents i < count.  A workgroup owns 32 sampled latents x 32
+// rows; its four waves take interleaved quarters of the d-steps and their fp32
+// partial sums are added in a fixed order (deterministic).  Operands are read
+// straight from global memory (W rows once, X rows from L2).
 // ---------------------------------------------------------------------------
-template <int DT, int NB>
-__global__ __launch_bounds__(kThreads, 1) void sample_kernel(SampleArgs a)
+template <int DT>
+__global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a)
 {
-    constexpr int BT = 32 * NB;
     constexpr int ES = Dt<DT>::esize;
     constexpr int DS = Dt<DT>::DS;
-    __shared__ __align__(16) unsigned char xs[2 * BT * kXRowStride];
+    __shared__ float red[kWaves - 1][16][64 + 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, jl = lane & 31;
-    const int64_t b0 = (int64_t)blockIdx.z * BT;
-    const int64_t ib = (int64_t)blockIdx.x * 128 + wave * 32;
-    const int64_t nds = (a.d + DS - 1) / DS;
-    const int64_t s0 = (int64_t)blockIdx.y * a.steps_per_split;
-    const int64_t s1 = (s0 + a.steps_per_split < nds) ? s0 + a.steps_per_split : nds;
+    const int64_t ib = (int64_t)blockIdx.x * 32;
+    const int64_t jb = (int64_t)blockIdx.y * 32;
+    const int64_t d = a.d;
+    const int64_t nds = (d + DS - 1) / DS;
 
-    MainLoop<DT, NB, 1> ml;
-    ml.X = (const unsigned char*)a.X;
-    ml.B = a.B;
-    ml.d = a.d;
-    ml.b0 = b0;
-    ml.lane = lane;
-    ml.h = h;
     int64_t i = ib + jl;
     i = (i < a.count) ? i : a.count - 1;
-    ml.wrow[0] = (const unsigned char*)a.W + (i << a.samp_log2) * a.d * ES + h * 64;
+    const unsigned char* wp = (const unsigned char*)a.W + (i << a.samp_log2) * d * ES + h * 64;
+    const int64_t j = jb + jl;
+    const bool jok = j < a.B;
+    const unsigned char* xp = (const unsigned char*)a.X + (jok ? j : 0) * d * ES + h * 64;
 
-    f32x16 acc[1][NB];
+    f32x16 acc;
 #pragma unroll
-    for (int n = 0; n < NB; ++n)
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    for (int64_t s0 = wave; s0 < nds; s0 += 4 * kWaves) {
+        u32x4 wq[4][4], xq[4][4];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[0][n][r] = 0.f;
-    ml.run(acc, s0, s1, xs, xs + BT * kXRowStride, tid);
-
+        for (int t = 0; t < 4; ++t) {
+            const int64_t s = s0 + t * kWaves;
 #pragma unroll
-    for (int n = 0; n < NB; ++n) {
-        const int64_t j = b0 + 32 * n + jl;
-        if (j >= a.B) continue;
-        float* prow = a.P + ((int64_t)blockIdx.y * a.B + j) * a.count;
+            for (int q = 0; q < 4; ++q) {
+                const int64_t e0 = s * DS + h * (DS / 2) + q * (DS / 8);
+                const bool ok = s < nds && e0 < d;
+                wq[t][q] = ok ? *(const u32x4*)(wp + s * kStepBytes + q * 16) : u32x4{0u, 0u, 0u, 0u};
+                xq[t][q] = (ok && jok) ? *(const u32x4*)(xp + s * kStepBytes + q * 16) : u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) mfma_quad<DT>(acc, wq[t][q], xq[t][q]);
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[wave - 1][r][lane] = acc[r];
+    }
+    __syncthreads();
+    if (wave == 0 && jok) {
+        float* prow = a.P + j * a.count;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int64_t ii = ib + (r >> 2) * 8 + h * 4 + (r & 3);
-            if (ii < a.count) prow[ii] = acc[0][n][r];
+            if (ii < a.count) {
+                const float s = ((acc[r] + red[0][r][lane]) + red[1][r][lane]) + red[2][r][lane];
+                prow[ii] = s + a.bias[ii << a.samp_log2];
+            }
         }
     }
 }
@@ -262,45 +254,33 @@ __device__ inline void append_key(SelShared& S, uint64_t key, bool& stalled)
         stalled = true;
 }
 
-// Per row: top-k of the sample scores (sum of split partials + bias).
+// Per row: exact top-k of the sampled scores -> seed keys and row threshold.
 __global__ __launch_bounds__(kThreads) void seed_kernel(SeedArgs a)
 {
+    constexpr int kItems = kSampleTarget / kThreads;
     __shared__ SelShared S;
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
     const int k = a.k;
-    if (tid == 0) { S.cnt = 0; S.thr = 0; }
-    __syncthreads();
-    int64_t cur = tid;   // next sample index for this thread
-    for (;;) {
-        const uint64_t thr = S.thr;
-        bool stalled = false;
-        while (cur < a.count) {
-            float s = 0.f;
-            for (int sp = 0; sp < a.nsplit; ++sp) s += a.P[((int64_t)sp * a.B + row) * a.count + cur];
-            const int64_t f = cur << a.samp_log2;
-            s += a.bias[f];
-            const uint64_t key = make_key(s, f);
-            if (key > thr) {
-                append_key(S, key, stalled);
-                if (stalled) break;
-            }
-            cur += kThreads;
-        }
-        __syncthreads();
-        if (S.cnt >= kSelCap) select_compact(S, kSelCap, k, tid);
-        if (!__syncthreads_or(stalled)) break;
+    const float* prow = a.P + row * a.count;
+    uint64_t key[kItems];
+    uint64_t m = 0;
+#pragma unroll
+    for (int t = 0; t < kItems; ++t) {
+        const int64_t i = tid + (int64_t)t * kThreads;
+        key[t] = (i < a.count) ? make_key(prow[i], i << a.samp_log2) : 0ull;
+        m = key[t] > m ? key[t] : m;
     }
-    const int n = S.cnt < kSelCap ? S.cnt : kSelCap;
-    if (n > k) select_compact(S, n, k, tid);
-    __syncthreads();
-    const int m = n < k ? n : k;
-    if (tid < m) {
-        const uint64_t key = S.buf[tid];
-        const int r = rank_desc(S, m, key);
-        a.seed_keys[row * k + r] = key;
-        if (r == k - 1) a.thr[row] = key;
-    }
+    if (tid == 0) S.cnt = 0;
+    const uint64_t T = kth_of_maxima(S, m, k, tid);
+    bool stalled = false;
+#pragma unroll
+    for (int t = 0; t < kItems; ++t)
+        if (key[t] != 0 && key[t] >= T) append_key(S, key[t], stalled);
+    emit_topk(S, k, tid, [&](int r, uint64_t kk) {
+        a.seed_keys[row * k + r] = kk;
+        if (r == k - 1) a.thr[row] = kk;
+    });
 }
 
 // Per row: top-k of the seed keys plus every main_kernel workgroup queue.
@@ -310,27 +290,41 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
     const int k = a.k;
-    if (tid == 0) { S.cnt = 0; S.thr = 0; }
-    __syncthreads();
-    if (a.seed_keys != nullptr) {
-        // the seed holds exactly k keys (the sample has at least k latents)
-        if (tid < k) S.buf[tid] = a.seed_keys[row * k + tid];
-        if (tid == 0) { S.cnt = k; S.thr = a.seed_keys[row * k + k - 1]; }
-        __syncthreads();
+    // pass 1: each thread's largest key (seed entry tid, segments tid + 256 j)
+    uint64_t m = 0;
+    if (a.seed_keys != nullptr && tid < k) m = a.seed_keys[row * k + tid];
+    for (int64_t seg = tid; seg < a.nseg; seg += kThreads) {
+        const int64_t sid = row * a.nseg + seg;
+        const int c = a.seg_cnt[sid];
+        const uint64_t* keys = a.seg_keys + sid * a.cap;
+#pragma unroll 8
+        for (int e = 0; e < c; ++e) {
+            const uint64_t kk = keys[e];
+            m = kk > m ? kk : m;
+        }
     }
-    int64_t seg = tid;   // segment cursor
-    int e = 0;           // entry cursor within the segment
+    if (tid == 0) S.cnt = 0;
+    const uint64_t T = kth_of_maxima(S, m, k, tid);
+    // pass 2: append every key >= the running threshold; compact when full
+    bool seed_done = !(a.seed_keys != nullptr && tid < k);
+    int64_t seg = tid;
+    int e = 0;
     for (;;) {
-        const uint64_t thr = S.thr;
+        const uint64_t thr = S.thr > T ? S.thr : T;
         bool stalled = false;
-        while (seg < a.nseg) {
+        if (!seed_done) {
+            const uint64_t kk = a.seed_keys[row * k + tid];
+            if (kk >= thr) append_key(S, kk, stalled);
+            seed_done = !stalled;
+        }
+        while (!stalled && seg < a.nseg) {
             const int64_t sid = row * a.nseg + seg;
             const int c = a.seg_cnt[sid];
             const uint64_t* keys = a.seg_keys + sid * a.cap;
             while (e < c) {
-                const uint64_t key = keys[e];
-                if (key > thr) {
-                    append_key(S, key, stalled);
+                const uint64_t kk = keys[e];
+                if (kk >= thr) {
+                    append_key(S, kk, stalled);
                     if (stalled) break;
                 }
                 ++e;
@@ -343,16 +337,10 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
         if (S.cnt >= kSelCap) select_compact(S, kSelCap, k, tid);
         if (!__syncthreads_or(stalled)) break;
     }
-    const int n = S.cnt < kSelCap ? S.cnt : kSelCap;
-    if (n > k) select_compact(S, n, k, tid);
-    __syncthreads();
-    const int m = n < k ? n : k;
-    if (tid < m) {
-        const uint64_t key = S.buf[tid];
-        const int r = rank_desc(S, m, key);
-        a.V[row * k + r] = key_value(key);
-        a.I[row * k + r] = key_index(key);
-    }
+    emit_topk(S, k, tid, [&](int r, uint64_t kk) {
+        a.V[row * k + r] = key_value(kk);
+        a.I[row * k + r] = key_index(kk);
+    });
 }
 
 // ---------------------------------------------------------------------------
@@ -371,7 +359,7 @@ static hipError_t launch_main_t(const MainArgs& a, dim3 grid, hipStream_t st)
     auto kern = main_kernel<DT, NB>;
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, st, a);
+    hipLaunchKernelGGL(kern, grid, dim3(kMainThreads), lds, st, a);
     return hipGetLastError();
 }
 
@@ -386,22 +374,13 @@ hipError_t launch_main(int dt, int NB, const MainArgs& a, dim3 grid, hipStream_t
     return hipErrorInvalidValue;
 }
 
-template <int DT, int NB>
-static hipError_t launch_sample_t(const SampleArgs& a, dim3 grid, hipStream_t st)
+hipError_t launch_sample(int dt, const SampleArgs& a, dim3 grid, hipStream_t st)
 {
-    hipLaunchKernelGGL((sample_kernel<DT, NB>), grid, dim3(kThreads), 0, st, a);
+    if (dt == DT_BF16) hipLaunchKernelGGL(sample_kernel<DT_BF16>, grid, dim3(kThreads), 0, st, a);
+    else if (dt == DT_F16) hipLaunchKernelGGL(sample_kernel<DT_F16>, grid, dim3(kThreads), 0, st, a);
+    else if (dt == DT_F32) hipLaunchKernelGGL(sample_kernel<DT_F32>, grid, dim3(kThreads), 0, st, a);
+    else return hipErrorInvalidValue;
     return hipGetLastError();
-}
-
-hipError_t launch_sample(int dt, int NB, const SampleArgs& a, dim3 grid, hipStream_t st)
-{
-#define STK_CASE(DTV, NBV) \
-    if (dt == DTV && NB == NBV) return launch_sample_t<DTV, NBV>(a, grid, st);
-    STK_CASE(DT_BF16, 1) STK_CASE(DT_BF16, 2) STK_CASE(DT_BF16, 4)
-    STK_CASE(DT_F16, 1) STK_CASE(DT_F16, 2) STK_CASE(DT_F16, 4)
-    STK_CASE(DT_F32, 1) STK_CASE(DT_F32, 2) STK_CASE(DT_F32, 4)
-#undef STK_CASE
-    return hipErrorInvalidValue;
 }
 
 hipError_t launch_seed(const SeedArgs& a, int64_t rows, hipStream_t st)

@@ -13,10 +13,35 @@ struct SelShared {
     uint64_t buf[kSelCap];
     uint32_t hist[kWaves][256];
     uint64_t sel[kMaxK];
+    uint64_t tmax[kThreads];
     uint64_t prefix, mask, thr;
     uint32_t remaining;
     int cnt, sel_cnt, done;
 };
+
+constexpr int kRankMax = 512;   // candidates ranked directly (more -> radix select first)
+
+// Every thread passes the largest key it holds (0 if none).  Returns a key T
+// such that at least min(k, #keys) keys are >= T: the k-th largest of the
+// per-thread maxima (those k maxima are themselves >= T), or 1 (accept every
+// real key) when fewer than k threads hold a key.
+__device__ inline uint64_t kth_of_maxima(SelShared& S, uint64_t m, int k, int tid)
+{
+    S.tmax[tid] = m;
+    if (tid == 0) S.thr = 1;
+    const int nz = __syncthreads_count(m != 0);
+    if (nz < k) return 1;
+    if (m != 0) {
+        int r = 0;
+        for (int i = 0; i < kThreads; i += 2) {
+            const u64x2 v = *(const u64x2*)(S.tmax + i);
+            r += (int)(v[0] > m) + (int)(v[1] > m);
+        }
+        if (r == k - 1) S.thr = m;
+    }
+    __syncthreads();
+    return S.thr;
+}
 
 // Finds the digit prefix of the k-th largest key among buf[0..n): afterwards
 // exactly k keys satisfy (key & S.mask) >= S.prefix.  Requires n >= k >= 1.
@@ -104,12 +129,37 @@ __device__ inline void select_compact(SelShared& S, int n, int k, int tid)
     __syncthreads();
 }
 
-// Rank of buf[t] among buf[0..n) in descending key order (keys are unique).
+// Rank of `key` among buf[0..n) in descending key order (keys are unique).
 __device__ inline int rank_desc(const SelShared& S, int n, uint64_t key)
 {
     int r = 0;
-    for (int i = 0; i < n; ++i) r += (S.buf[i] > key) ? 1 : 0;
+    int i = 0;
+    for (; i + 1 < n; i += 2) {
+        const u64x2 v = *(const u64x2*)(S.buf + i);
+        r += (int)(v[0] > key) + (int)(v[1] > key);
+    }
+    if (i < n) r += (int)(S.buf[i] > key);
     return r;
+}
+
+// Reduces buf[0..cnt) to its top k and calls emit(rank, key) for rank < k,
+// rank 0 being the largest.  Returns the number of keys emitted.
+template <class Emit>
+__device__ inline int emit_topk(SelShared& S, int k, int tid, Emit emit)
+{
+    __syncthreads();
+    int n = S.cnt < kSelCap ? S.cnt : kSelCap;
+    if (n > kRankMax) {
+        select_compact(S, n, k, tid);
+        n = k;
+    }
+    __syncthreads();
+    for (int i = tid; i < n; i += kThreads) {
+        const uint64_t key = S.buf[i];
+        const int r = rank_desc(S, n, key);
+        if (r < k) emit(r, key);
+    }
+    return n < k ? n : k;
 }
 
 }  // namespace stk

@@ -115,7 +115,8 @@ def _prepare_device(X, W_enc, b_enc):
     W_enc = W_enc.contiguous()
     b_enc = b_enc.contiguous()
     _device_checks(X, W_enc, b_enc)
-    multiple = 4 if X.dtype == torch.float32 else 8
+    # the kernels stream 128-byte d-steps: 32 fp32 or 64 fp16/bf16 elements
+    multiple = 32 if X.dtype == torch.float32 else 64
     X, W_enc = _pad_d(X, W_enc, multiple)
     return _aligned(X), _aligned(W_enc), b_enc
 
