@@ -313,18 +313,23 @@ struct TileStream {
     __device__ __forceinline__ void compute(f32x16 (&acc)[FRAGS][NB], const u32x4 (&w)[FRAGS][4],
                                             const unsigned char* xs) const
     {
-        u32x4 bx[NB][4];
+        // two 32-row blocks at a time: two independent accumulation chains
+        constexpr int NP = NB < 2 ? NB : 2;
 #pragma unroll
-        for (int n = 0; n < NB; ++n)
+        for (int n0 = 0; n0 < NB; n0 += NP) {
+            u32x4 bx[NP][4];
+#pragma unroll
+            for (int n = 0; n < NP; ++n)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    bx[n][q] = *(const u32x4*)(xs + (32 * (n0 + n) + jl) * kXRowStride + h * 64 + q * 16);
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                bx[n][q] = *(const u32x4*)(xs + (32 * n + jl) * kXRowStride + h * 64 + q * 16);
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+                for (int n = 0; n < NP; ++n)
 #pragma unroll
-            for (int n = 0; n < NB; ++n)
-#pragma unroll
-                for (int a = 0; a < FRAGS; ++a) mfma_quad<DT>(acc[a][n], w[a][q], bx[n][q]);
+                    for (int a = 0; a < FRAGS; ++a) mfma_quad<DT>(acc[a][n0 + n], w[a][q], bx[n][q]);
+        }
     }
 
     // Bias of this lane's latents of tile t: entry [a][r] is latent

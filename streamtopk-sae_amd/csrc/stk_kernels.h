@@ -5,7 +5,7 @@
 
 namespace stk {
 
-constexpr int kMainWaves = 4;        // wavefronts per main_kernel workgroup (1 per SIMD)
+constexpr int kMainWaves = 8;        // wavefronts per main_kernel workgroup (2 per SIMD)
 constexpr int kMainThreads = 64 * kMainWaves;
 constexpr int kTileLatents = 32 * kMainWaves;   // latents per main_kernel tile
 constexpr int kApproxGroup = 128;    // latent group of the approximate variant

@@ -23,7 +23,7 @@ namespace stk {
 // main_kernel
 // ---------------------------------------------------------------------------
 template <int DT, int NB>
-__global__ __launch_bounds__(kMainThreads, 1) void main_kernel(MainArgs a)
+__global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
 {
     constexpr int BT = 32 * NB;
     constexpr int FRAGS = 1;
@@ -68,37 +68,40 @@ __global__ __launch_bounds__(kMainThreads, 1) void main_kernel(MainArgs a)
     ts.init_x((const unsigned char*)a.X, B, b0, a.d);
     const int64_t smask = a.samp_count ? ((int64_t)1 << a.samp_log2) - 1 : 0;
 
+    constexpr int kRowsPerWave = BT / WAVES;   // queue rows this wave compacts (<= 64)
     f32x16 acc[FRAGS][NB];
     ts.run(acc, xs0, xs1, [&](int t, f32x16 (&ac)[FRAGS][NB], const float (&bias_r)[FRAGS][16]) {
-        // this lane's latent for accumulator register r
-        const int64_t fw0 = (ts.tile_begin + t) * kTileLatents + wave * 32 + h * 4;
-        // ---- filter against the row thresholds ----
+        // latent of accumulator register r of this lane: fl + 8*(r/4) + r%4
+        const int64_t fl = (ts.tile_begin + t) * (int64_t)kTileLatents + wave * 32 + h * 4;
         uint32_t vmask = 0;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int64_t f = fw0 + (r >> 2) * 8 + (r & 3);
+            const int64_t f = fl + (r >> 2) * 8 + (r & 3);
             bool ok = f < F;
             if (a.samp_count && (f & smask) == 0 && (f >> a.samp_log2) < a.samp_count) ok = false;
-            if (ok) vmask |= 1u << r;
+            vmask |= ok ? (1u << r) : 0u;
         }
+        // ---- filter against the row thresholds (float pre-check, exact key check) ----
         uint32_t pend[NB];
-        uint64_t thr_r[NB];
 #pragma unroll
         for (int n = 0; n < NB; ++n) {
             const int j = 32 * n + jl;
-            thr_r[n] = thr[j];
-            pend[n] = 0;
-            if (b0 + j < B) {
-                const float tv = key_value(thr_r[n]);
-                const bool all = thr_r[n] == 0ull;
+            const uint64_t tk = thr[j];
+            const float tv = tk ? key_value(tk) : -__builtin_inff();
+            uint32_t m = 0;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const float sc = ac[0][n][r] + bias_r[0][r];
-                    if ((vmask >> r & 1u) && (all || !(sc < tv))) {
-                        if (make_key(sc, fw0 + (r >> 2) * 8 + (r & 3)) > thr_r[n]) pend[n] |= 1u << r;
-                    }
-                }
+            for (int r = 0; r < 16; ++r) {
+                const float sc = ac[0][n][r] + bias_r[0][r];
+                m |= (!(sc < tv)) ? (1u << r) : 0u;
             }
+            m &= (b0 + j < B) ? vmask : 0u;
+            if (m && tk) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if ((m >> r & 1u) && !(make_key(ac[0][n][r] + bias_r[0][r], fl + (r >> 2) * 8 + (r & 3)) > tk))
+                        m &= ~(1u << r);
+            }
+            pend[n] = m;
         }
 
         // ---- append / compact until every passing score is placed or dropped ----
@@ -107,33 +110,43 @@ __global__ __launch_bounds__(kMainThreads, 1) void main_kernel(MainArgs a)
 #pragma unroll
             for (int n = 0; n < NB; ++n) any |= pend[n];
             if (!__syncthreads_or(any != 0)) break;
+            // one slot reservation per (lane, row), then predicated stores
 #pragma unroll
             for (int n = 0; n < NB; ++n) {
                 if (pend[n] == 0) continue;
                 const int j = 32 * n + jl;
+                const int pos = atomicAdd(&cnt[j], __builtin_popcount(pend[n]));
+                uint64_t* qj = q + (size_t)j * cap;
+                int slot = pos;
+                uint32_t keep = 0;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     if (pend[n] >> r & 1u) {
-                        const uint64_t key = make_key(ac[0][n][r] + bias_r[0][r], fw0 + (r >> 2) * 8 + (r & 3));
-                        const int pos = atomicAdd(&cnt[j], 1);
-                        if (pos < cap) {
-                            q[(size_t)j * cap + pos] = key;
-                            pend[n] &= ~(1u << r);
-                        }
+                        if (slot < cap)
+                            qj[slot] = make_key(ac[0][n][r] + bias_r[0][r], fl + (r >> 2) * 8 + (r & 3));
+                        else
+                            keep |= 1u << r;
+                        ++slot;
                     }
                 }
+                pend[n] = keep;
             }
             __syncthreads();
-            for (int row = wave; row < BT; row += WAVES) {
-                if (cnt[row] >= cap) {
-                    // wave-wide rank compaction of a full queue to its top-k
+            // wave w compacts its rows w*kRowsPerWave + i whose queue is full
+            {
+                const int myrow = wave * kRowsPerWave + (lane < kRowsPerWave ? lane : 0);
+                uint64_t full = __ballot(lane < kRowsPerWave && cnt[myrow] >= cap);
+                while (full) {
+                    const int i = __builtin_ctzll(full);
+                    full &= full - 1;
+                    const int row = wave * kRowsPerWave + i;
                     uint64_t* qr = q + (size_t)row * cap;
                     uint64_t e[3];
                     int rk[3] = {0, 0, 0};
 #pragma unroll
                     for (int m = 0; m < 3; ++m) e[m] = (lane + 64 * m < cap) ? qr[lane + 64 * m] : 0ull;
-                    for (int i = 0; i < cap; i += 2) {
-                        const u64x2 v = *(const u64x2*)(qr + i);
+                    for (int ii = 0; ii < cap; ii += 2) {
+                        const u64x2 v = *(const u64x2*)(qr + ii);
 #pragma unroll
                         for (int m = 0; m < 3; ++m) rk[m] += (int)(v[0] > e[m]) + (int)(v[1] > e[m]);
                     }
@@ -148,17 +161,15 @@ __global__ __launch_bounds__(kMainThreads, 1) void main_kernel(MainArgs a)
                 }
             }
             __syncthreads();
+            // drop pending scores that fell below a raised threshold
 #pragma unroll
             for (int n = 0; n < NB; ++n) {
                 if (pend[n] == 0) continue;
-                thr_r[n] = thr[32 * n + jl];
+                const uint64_t tk = thr[32 * n + jl];
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    if (pend[n] >> r & 1u) {
-                        if (!(make_key(ac[0][n][r] + bias_r[0][r], fw0 + (r >> 2) * 8 + (r & 3)) > thr_r[n]))
-                            pend[n] &= ~(1u << r);
-                    }
-                }
+                for (int r = 0; r < 16; ++r)
+                    if ((pend[n] >> r & 1u) && !(make_key(ac[0][n][r] + bias_r[0][r], fl + (r >> 2) * 8 + (r & 3)) > tk))
+                        pend[n] &= ~(1u << r);
             }
         }
     });
