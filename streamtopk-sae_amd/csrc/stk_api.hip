@@ -112,7 +112,6 @@ struct ExactPlan {
     int64_t nbc, num_tiles, tpw;
     int nwg;
     bool sample;
-    int64_t samp_count;
     int samp_log2;
     size_t off_seed, off_thr, off_P, off_keys, off_cnt, total;
 };
@@ -137,15 +136,10 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
     p.nwg = (int)cdiv(p.num_tiles, p.tpw);
 
     p.sample = F >= kSampleMinF;
-    p.samp_count = 0;
     p.samp_log2 = 0;
     if (p.sample) {
-        // every (1 << samp_log2)-th latent, at most kSampleTarget of them
-        int l = ilog2_floor(F / kSampleTarget);
-        if (l < 4) l = 4;
-        p.samp_log2 = l;
-        p.samp_count = F >> l;
-        if (p.samp_count > kSampleTarget) p.samp_count = kSampleTarget;
+        // kSampleBlocks blocks of kSampleBlock consecutive latents, 1 << samp_log2 apart
+        p.samp_log2 = ilog2_floor(F / kSampleBlocks);
     }
     size_t off = 0;
     p.off_seed = off;
@@ -153,7 +147,7 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
     p.off_thr = off;
     if (p.sample) off = align256(off + (size_t)B * 8);
     p.off_P = off;
-    if (p.sample) off = align256(off + (size_t)B * p.samp_count * 4);
+    if (p.sample) off = align256(off + (size_t)B * kSampleTarget * 4);
     p.off_keys = off;
     off = align256(off + (size_t)B * p.nwg * p.cap * 8);
     p.off_cnt = off;
@@ -215,14 +209,14 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     if (p.sample) {
         SampleArgs sa;
         sa.X = X; sa.W = W; sa.bias = b; sa.B = B; sa.d = d;
-        sa.count = p.samp_count; sa.samp_log2 = p.samp_log2;
+        sa.samp_log2 = p.samp_log2;
         sa.P = (float*)(ws + p.off_P);
         int pi = prof_begin("sample_kernel", st);
-        e = launch_sample(dt, sa, dim3((unsigned)cdiv(p.samp_count, 32), (unsigned)cdiv(B, 32)), st);
+        e = launch_sample(dt, sa, dim3((unsigned)(kSampleTarget / 32), (unsigned)cdiv(B, 32)), st);
         prof_end(pi, st);
         if (e != hipSuccess) return hip_fail(e, "sample_kernel launch");
         SeedArgs sd;
-        sd.P = sa.P; sd.count = p.samp_count;
+        sd.P = sa.P;
         sd.samp_log2 = p.samp_log2; sd.k = (int)k;
         sd.seed_keys = seed; sd.thr = thr;
         pi = prof_begin("seed_kernel", st);
@@ -235,7 +229,7 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     ma.k = (int)k; ma.cap = p.cap;
     ma.num_tiles = p.num_tiles; ma.tiles_per_wg = p.tpw; ma.nwg = p.nwg;
     ma.thr0 = p.sample ? thr : nullptr;
-    ma.samp_count = p.sample ? p.samp_count : 0;
+    ma.sampled = p.sample ? 1 : 0;
     ma.samp_log2 = p.samp_log2;
     ma.out_keys = (uint64_t*)(ws + p.off_keys);
     ma.out_cnt = (int32_t*)(ws + p.off_cnt);

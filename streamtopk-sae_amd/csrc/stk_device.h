@@ -218,20 +218,21 @@ struct MainLoop {
 // ---------------------------------------------------------------------------
 // TileStream: the score main loop as one flat stream of d-steps over all the
 // tiles a workgroup owns.  A tile is 32*FRAGS*WAVES latents x 32*NB rows and
-// takes nds4 d-steps: the nds = d / DS real ones (d is a multiple of the
-// d-step) rounded up to a multiple of 4; the padding steps load a valid step
-// again and skip their MFMAs.  Four register sets of W (and of X) keep the
-// loads of the next three d-steps in flight -- across tile boundaries too.
+// takes nds3 d-steps: the nds = d / DS real ones (d is a multiple of the
+// d-step) rounded up to a multiple of 3; the padding steps load a valid step
+// again and skip their MFMAs.  Three register sets of W (and of X) keep the
+// loads of the next two d-steps in flight -- across tile boundaries too.
 // Every load is unconditional (rows past F or B and steps past the end are
 // clamped to valid addresses; the scores they produce are never selected), so
-// the in-order vmcnt waits never drain the prefetched W loads.  X is staged
-// through two LDS buffers (one barrier per d-step).
+// the in-order vmcnt waits never drain the prefetched W loads.  X goes
+// through a ring of three LDS buffers (one barrier per d-step).
 //
 // run() calls epi(t, acc, bias) after the last d-step of tile t (0-based
 // within the workgroup's tiles) and then clears acc.  The epilogue may use LDS
-// other than the two X buffers and must not issue global loads (waiting for
-// one would also wait for every older prefetched W load); the bias of tile t
-// it receives was loaded during the previous tile.
+// other than the X buffers and must neither issue global loads nor spill
+// registers (a scratch reload, like a global load, waits for every older
+// prefetched W load); the bias of tile t it receives was loaded during the
+// previous tile.
 // ---------------------------------------------------------------------------
 template <int DT, int NB, int FRAGS, int WAVES>
 struct TileStream {
@@ -246,7 +247,7 @@ struct TileStream {
     const float* bias;
     int64_t F;
     int64_t tile_begin;
-    int ntiles, nds, nds4;
+    int ntiles, nds, nds3;
     int tid, lane, wave, h, jl;
     const unsigned char* W;
     int64_t w_row_bytes;
@@ -293,7 +294,7 @@ struct TileStream {
 #pragma unroll
             for (int q = 0; q < 4; ++q) w[a][q] = *(const u32x4*)(pw + q * 16);
         }
-        if (lt < ntiles && ++ls == nds4) {
+        if (lt < ntiles && ++ls == nds3) {
             ls = 0;
             ++lt;
             if (lt < ntiles) set_rows(lt);
@@ -348,20 +349,19 @@ struct TileStream {
 
     template <class Epi>
     __device__ __forceinline__ void run(f32x16 (&acc)[FRAGS][NB], unsigned char* xs0, unsigned char* xs1,
-                                        Epi epi)
+                                        unsigned char* xs2, Epi epi)
     {
         if (ntiles <= 0) return;
         lt = 0;
         ls = 0;
         set_rows(0);
-        u32x4 w0[FRAGS][4], w1[FRAGS][4], w2[FRAGS][4], w3[FRAGS][4];
-        u32x4 x0[kXChunks], x1[kXChunks], x2[kXChunks], x3[kXChunks];
+        u32x4 w0[FRAGS][4], w1[FRAGS][4], w2[FRAGS][4];
+        u32x4 x0[kXChunks], x1[kXChunks], x2[kXChunks];
         float bv[FRAGS][16];
         tile_bias(bv, 0);
         issue(x0, w0);
         issue(x1, w1);
         issue(x2, w2);
-        issue(x3, w3);
         store_x(x0, xs0);
 #pragma unroll
         for (int a = 0; a < FRAGS; ++a)
@@ -371,22 +371,18 @@ struct TileStream {
                 for (int r = 0; r < 16; ++r) acc[a][n][r] = 0.f;
         __syncthreads();
         for (int t = 0; t < ntiles; ++t) {
-            for (int s = 0; s < nds4; s += 4) {
+            for (int s = 0; s < nds3; s += 3) {
                 store_x(x1, xs1);
                 if (s < nds) compute(acc, w0, xs0);
                 issue(x0, w0);
                 __syncthreads();
-                store_x(x2, xs0);
+                store_x(x2, xs2);
                 if (s + 1 < nds) compute(acc, w1, xs1);
                 issue(x1, w1);
                 __syncthreads();
-                store_x(x3, xs1);
-                if (s + 2 < nds) compute(acc, w2, xs0);
-                issue(x2, w2);
-                __syncthreads();
                 store_x(x0, xs0);
-                if (s + 3 < nds) compute(acc, w3, xs1);
-                issue(x3, w3);
+                if (s + 2 < nds) compute(acc, w2, xs2);
+                issue(x2, w2);
                 __syncthreads();
             }
             epi(t, acc, bv);

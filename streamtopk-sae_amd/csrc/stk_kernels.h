@@ -11,7 +11,23 @@ constexpr int kTileLatents = 32 * kMainWaves;   // latents per main_kernel tile
 constexpr int kApproxGroup = 128;    // latent group of the approximate variant
 constexpr int kGroupTile = 256;      // latents per group_kernel tile (two groups)
 constexpr int kSampleTarget = 4096;  // sampled latents that seed the thresholds
+constexpr int kSampleBlock = 128;    // consecutive latents per sampled block
+constexpr int kSampleBlocks = kSampleTarget / kSampleBlock;
 constexpr int64_t kSampleMinF = 16384;
+
+// Sampled latent i (0 <= i < kSampleTarget) is latent
+// (i / kSampleBlock) << blk_log2 + i % kSampleBlock: kSampleBlocks blocks of
+// consecutive latents spread evenly over F.
+__host__ __device__ inline int64_t sample_latent(int64_t i, int blk_log2)
+{
+    return ((i / kSampleBlock) << blk_log2) + (i % kSampleBlock);
+}
+
+// Whether latent f belongs to the sample.
+__host__ __device__ inline bool is_sampled(int64_t f, int blk_log2)
+{
+    return (f & ((int64_t(1) << blk_log2) - 1)) < kSampleBlock && (f >> blk_log2) < kSampleBlocks;
+}
 
 struct MainArgs {
     const void* X;
@@ -22,8 +38,8 @@ struct MainArgs {
     int64_t num_tiles, tiles_per_wg;
     int nwg;
     const uint64_t* thr0;        // per-row starting threshold keys, or null
-    int64_t samp_count;          // latents f = i << samp_log2, i < samp_count, are
-    int samp_log2;               //   scored by the sample pass and skipped here
+    int sampled;                 // non-zero: the sampled latents (is_sampled) were
+    int samp_log2;               //   scored by the sample pass and are skipped here
     uint64_t* out_keys;          // [B][nwg][cap]
     int32_t* out_cnt;            // [B][nwg]
 };
@@ -33,14 +49,12 @@ struct SampleArgs {
     const void* W;
     const float* bias;
     int64_t B, d;
-    int64_t count;
     int samp_log2;
-    float* P;                    // [B][count] scores of the sampled latents
+    float* P;                    // [B][kSampleTarget] scores of the sampled latents
 };
 
 struct SeedArgs {
     const float* P;
-    int64_t count;
     int samp_log2, k;
     uint64_t* seed_keys;         // [B][k], descending
     uint64_t* thr;               // [B]

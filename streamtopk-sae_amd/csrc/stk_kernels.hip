@@ -32,7 +32,8 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
     extern __shared__ __align__(16) unsigned char smem[];
     unsigned char* xs0 = smem;
     unsigned char* xs1 = smem + BT * kXRowStride;
-    uint64_t* q = (uint64_t*)(smem + 2 * BT * kXRowStride);
+    unsigned char* xs2 = smem + 2 * BT * kXRowStride;
+    uint64_t* q = (uint64_t*)(smem + 3 * BT * kXRowStride);
     const int cap = a.cap;
     uint64_t* thr = q + (size_t)BT * cap;
     int* cnt = (int*)(thr + BT);
@@ -59,29 +60,35 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
         ts.ntiles = (int)((t1 < a.num_tiles ? t1 : a.num_tiles) - ts.tile_begin);
     }
     ts.nds = (int)(a.d / DS);
-    ts.nds4 = (ts.nds + 3) & ~3;
+    ts.nds3 = (ts.nds + 2) / 3 * 3;
     ts.tid = tid;
     ts.lane = lane;
     ts.wave = wave;
     ts.h = h;
     ts.jl = jl;
     ts.init_x((const unsigned char*)a.X, B, b0, a.d);
-    const int64_t smask = a.samp_count ? ((int64_t)1 << a.samp_log2) - 1 : 0;
 
     constexpr int kRowsPerWave = BT / WAVES;   // queue rows this wave compacts (<= 64)
     f32x16 acc[FRAGS][NB];
-    ts.run(acc, xs0, xs1, [&](int t, f32x16 (&ac)[FRAGS][NB], const float (&bias_r)[FRAGS][16]) {
+    ts.run(acc, xs0, xs1, xs2, [&](int t, f32x16 (&ac)[FRAGS][NB], const float (&bias_r)[FRAGS][16]) {
         // latent of accumulator register r of this lane: fl + 8*(r/4) + r%4
-        const int64_t fl = (ts.tile_begin + t) * (int64_t)kTileLatents + wave * 32 + h * 4;
-        uint32_t vmask = 0;
+        const int64_t tile0 = (ts.tile_begin + t) * (int64_t)kTileLatents;
+        const int64_t fl = tile0 + wave * 32 + h * 4;
+        // latents past F or in the sample are never candidates here
+        uint32_t vmask = 0xFFFFu;
+        if (tile0 + kTileLatents > F || (a.sampled && (is_sampled(tile0, a.samp_log2) ||
+                                                       is_sampled(tile0 + kTileLatents - 1, a.samp_log2)))) {
+            vmask = 0;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t f = fl + (r >> 2) * 8 + (r & 3);
-            bool ok = f < F;
-            if (a.samp_count && (f & smask) == 0 && (f >> a.samp_log2) < a.samp_count) ok = false;
-            vmask |= ok ? (1u << r) : 0u;
+            for (int r = 0; r < 16; ++r) {
+                const int64_t f = fl + (r >> 2) * 8 + (r & 3);
+                const bool ok = f < F && !(a.sampled && is_sampled(f, a.samp_log2));
+                vmask |= ok ? (1u << r) : 0u;
+            }
         }
-        // ---- filter against the row thresholds (float pre-check, exact key check) ----
+        // ---- scores (bias added in place) not below the row threshold ----
+        // The float test keeps every score whose key beats the threshold key
+        // (and possibly a few equal to its value: harmless extra candidates).
         uint32_t pend[NB];
 #pragma unroll
         for (int n = 0; n < NB; ++n) {
@@ -91,47 +98,37 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
             uint32_t m = 0;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float sc = ac[0][n][r] + bias_r[0][r];
-                m |= (!(sc < tv)) ? (1u << r) : 0u;
+                ac[0][n][r] += bias_r[0][r];
+                m |= (!(ac[0][n][r] < tv)) ? (1u << r) : 0u;
             }
-            m &= (b0 + j < B) ? vmask : 0u;
-            if (m && tk) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    if ((m >> r & 1u) && !(make_key(ac[0][n][r] + bias_r[0][r], fl + (r >> 2) * 8 + (r & 3)) > tk))
-                        m &= ~(1u << r);
-            }
-            pend[n] = m;
+            pend[n] = (b0 + j < B) ? (m & vmask) : 0u;
         }
 
-        // ---- append / compact until every passing score is placed or dropped ----
+        // ---- append; compact full queues and retry while anything overflowed ----
         for (int it = 0; it < 4096; ++it) {
-            uint32_t any = 0;
-#pragma unroll
-            for (int n = 0; n < NB; ++n) any |= pend[n];
-            if (!__syncthreads_or(any != 0)) break;
-            // one slot reservation per (lane, row), then predicated stores
+            bool overflow = false;
 #pragma unroll
             for (int n = 0; n < NB; ++n) {
-                if (pend[n] == 0) continue;
+                const uint32_t m = pend[n];
+                if (m == 0) continue;
                 const int j = 32 * n + jl;
-                const int pos = atomicAdd(&cnt[j], __builtin_popcount(pend[n]));
+                const int base = atomicAdd(&cnt[j], __builtin_popcount(m));
                 uint64_t* qj = q + (size_t)j * cap;
-                int slot = pos;
                 uint32_t keep = 0;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    if (pend[n] >> r & 1u) {
+                    if (m >> r & 1u) {
+                        const int slot = base + __builtin_popcount(m & ((1u << r) - 1u));
                         if (slot < cap)
-                            qj[slot] = make_key(ac[0][n][r] + bias_r[0][r], fl + (r >> 2) * 8 + (r & 3));
+                            qj[slot] = make_key(ac[0][n][r], fl + (r >> 2) * 8 + (r & 3));
                         else
                             keep |= 1u << r;
-                        ++slot;
                     }
                 }
                 pend[n] = keep;
+                overflow |= keep != 0;
             }
-            __syncthreads();
+            if (!__syncthreads_or(overflow)) break;
             // wave w compacts its rows w*kRowsPerWave + i whose queue is full
             {
                 const int myrow = wave * kRowsPerWave + (lane < kRowsPerWave ? lane : 0);
@@ -144,17 +141,17 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
                     uint64_t e[3];
                     int rk[3] = {0, 0, 0};
 #pragma unroll
-                    for (int m = 0; m < 3; ++m) e[m] = (lane + 64 * m < cap) ? qr[lane + 64 * m] : 0ull;
+                    for (int mm = 0; mm < 3; ++mm) e[mm] = (lane + 64 * mm < cap) ? qr[lane + 64 * mm] : 0ull;
                     for (int ii = 0; ii < cap; ii += 2) {
                         const u64x2 v = *(const u64x2*)(qr + ii);
 #pragma unroll
-                        for (int m = 0; m < 3; ++m) rk[m] += (int)(v[0] > e[m]) + (int)(v[1] > e[m]);
+                        for (int mm = 0; mm < 3; ++mm) rk[mm] += (int)(v[0] > e[mm]) + (int)(v[1] > e[mm]);
                     }
 #pragma unroll
-                    for (int m = 0; m < 3; ++m) {
-                        if (lane + 64 * m < cap && rk[m] < k) {
-                            qr[rk[m]] = e[m];
-                            if (rk[m] == k - 1) thr[row] = e[m];
+                    for (int mm = 0; mm < 3; ++mm) {
+                        if (lane + 64 * mm < cap && rk[mm] < k) {
+                            qr[rk[mm]] = e[mm];
+                            if (rk[mm] == k - 1) thr[row] = e[mm];
                         }
                     }
                     if (lane == 0) cnt[row] = k;
@@ -168,7 +165,7 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
                 const uint64_t tk = thr[32 * n + jl];
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
-                    if ((pend[n] >> r & 1u) && !(make_key(ac[0][n][r] + bias_r[0][r], fl + (r >> 2) * 8 + (r & 3)) > tk))
+                    if ((pend[n] >> r & 1u) && !(make_key(ac[0][n][r], fl + (r >> 2) * 8 + (r & 3)) > tk))
                         pend[n] &= ~(1u << r);
             }
         }
@@ -188,8 +185,8 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
 }
 
 // ---------------------------------------------------------------------------
-// sample_kernel: P[row][i] = X[row] . W[i << samp_log2] + b[i << samp_log2]
-// for the sampled latents i < count.  A workgroup owns 32 sampled latents x 32
+// sample_kernel: P[row][i] = X[row] . W[f] + b[f], f = sample_latent(i), for
+// the kSampleTarget sampled latents.  A workgroup owns 32 sampled latents x 32
 // rows; its four waves take interleaved quarters of the d-steps and their fp32
 // partial sums are added in a fixed order (deterministic).  Operands are read
 // straight from global memory (W rows once, X rows from L2).
@@ -207,9 +204,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a)
     const int64_t d = a.d;
     const int64_t nds = (d + DS - 1) / DS;
 
-    int64_t i = ib + jl;
-    i = (i < a.count) ? i : a.count - 1;
-    const unsigned char* wp = (const unsigned char*)a.W + (i << a.samp_log2) * d * ES + h * 64;
+    const unsigned char* wp = (const unsigned char*)a.W + sample_latent(ib + jl, a.samp_log2) * d * ES + h * 64;
     const int64_t j = jb + jl;
     const bool jok = j < a.B;
     const unsigned char* xp = (const unsigned char*)a.X + (jok ? j : 0) * d * ES + h * 64;
@@ -241,14 +236,12 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a)
     }
     __syncthreads();
     if (wave == 0 && jok) {
-        float* prow = a.P + j * a.count;
+        float* prow = a.P + j * kSampleTarget;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int64_t ii = ib + (r >> 2) * 8 + h * 4 + (r & 3);
-            if (ii < a.count) {
-                const float s = ((acc[r] + red[0][r][lane]) + red[1][r][lane]) + red[2][r][lane];
-                prow[ii] = s + a.bias[ii << a.samp_log2];
-            }
+            const float s = ((acc[r] + red[0][r][lane]) + red[1][r][lane]) + red[2][r][lane];
+            prow[ii] = s + a.bias[sample_latent(ii, a.samp_log2)];
         }
     }
 }
@@ -273,13 +266,13 @@ __global__ __launch_bounds__(kThreads) void seed_kernel(SeedArgs a)
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
     const int k = a.k;
-    const float* prow = a.P + row * a.count;
+    const float* prow = a.P + row * kSampleTarget;
     uint64_t key[kItems];
     uint64_t m = 0;
 #pragma unroll
     for (int t = 0; t < kItems; ++t) {
         const int64_t i = tid + (int64_t)t * kThreads;
-        key[t] = (i < a.count) ? make_key(prow[i], i << a.samp_log2) : 0ull;
+        key[t] = make_key(prow[i], sample_latent(i, a.samp_log2));
         m = key[t] > m ? key[t] : m;
     }
     if (tid == 0) S.cnt = 0;
@@ -308,10 +301,12 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
         const int64_t sid = row * a.nseg + seg;
         const int c = a.seg_cnt[sid];
         const uint64_t* keys = a.seg_keys + sid * a.cap;
-#pragma unroll 8
-        for (int e = 0; e < c; ++e) {
-            const uint64_t kk = keys[e];
-            m = kk > m ? kk : m;
+        for (int e0 = 0; e0 < c; e0 += 8) {
+            uint64_t v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = (e0 + u < c) ? keys[e0 + u] : 0ull;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) m = v[u] > m ? v[u] : m;
         }
     }
     if (tid == 0) S.cnt = 0;
@@ -360,7 +355,7 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
 size_t main_lds_bytes(int NB, int cap)
 {
     const size_t BT = 32 * (size_t)NB;
-    return 2 * BT * kXRowStride + BT * (size_t)cap * 8 + BT * 8 + BT * 4;
+    return 3 * BT * kXRowStride + BT * (size_t)cap * 8 + BT * 8 + BT * 4;
 }
 
 template <int DT, int NB>

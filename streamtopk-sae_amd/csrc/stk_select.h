@@ -33,9 +33,12 @@ __device__ inline uint64_t kth_of_maxima(SelShared& S, uint64_t m, int k, int ti
     if (nz < k) return 1;
     if (m != 0) {
         int r = 0;
-        for (int i = 0; i < kThreads; i += 2) {
-            const u64x2 v = *(const u64x2*)(S.tmax + i);
-            r += (int)(v[0] > m) + (int)(v[1] > m);
+        for (int i = 0; i < kThreads; i += 16) {
+            u64x2 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = *(const u64x2*)(S.tmax + i + 2 * u);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) r += (int)(v[u][0] > m) + (int)(v[u][1] > m);
         }
         if (r == k - 1) S.thr = m;
     }
@@ -134,11 +137,14 @@ __device__ inline int rank_desc(const SelShared& S, int n, uint64_t key)
 {
     int r = 0;
     int i = 0;
-    for (; i + 1 < n; i += 2) {
-        const u64x2 v = *(const u64x2*)(S.buf + i);
-        r += (int)(v[0] > key) + (int)(v[1] > key);
+    for (; i + 16 <= n; i += 16) {
+        u64x2 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = *(const u64x2*)(S.buf + i + 2 * u);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) r += (int)(v[u][0] > key) + (int)(v[u][1] > key);
     }
-    if (i < n) r += (int)(S.buf[i] > key);
+    for (; i < n; ++i) r += (int)(S.buf[i] > key);
     return r;
 }
 
