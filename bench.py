@@ -50,27 +50,64 @@ def _cpu_cores():
 
 def cpu_baseline(X, W, b, k, seconds):
     """Times the oracle's restatement of the reference CPU kernel (OpenMP over
-    rows, each row streaming all of W) on the first rows of the same batch."""
+    rows, each row streaming all of W) over whole passes of the same batch,
+    repeated until about `seconds` of CPU work has been done."""
     import numpy as np
     import oracle
     cores = _cpu_cores()
-    Xf = X.float().cpu().numpy()
-    Wf = W.float().cpu().numpy()
-    bf = b.float().cpu().numpy()
-    rows = min(cores, Xf.shape[0])
-    t0 = time.perf_counter()
-    oracle.cpu_stream(Xf[:rows], Wf, bf, k, nthreads=cores)
-    t1 = time.perf_counter() - t0
-    reps = max(1, int(seconds / max(t1, 1e-3)))
-    rows2 = min(Xf.shape[0], rows * reps)
-    if rows2 > rows:
+    Xf = np.ascontiguousarray(X.float().cpu().numpy())
+    Wf = np.ascontiguousarray(W.float().cpu().numpy())
+    bf = np.ascontiguousarray(b.float().cpu().numpy())
+    passes, rows, t = 0, 0, 0.0
+    while t < seconds:
         t0 = time.perf_counter()
-        oracle.cpu_stream(Xf[:rows2], Wf, bf, k, nthreads=cores)
-        t1 = time.perf_counter() - t0
-        rows = rows2
-    return {"value": rows / t1, "unit": "rows/s", "cores": cores, "kind": "port",
-            "sample": f"rows 0..{rows - 1} of the same batch, full F and d, fp32 upcast inputs; "
-                      f"oracle/stk_oracle_cpu.c (reference streamtopk_cpu.cpp restated), {t1:.2f} s"}
+        oracle.cpu_stream(Xf, Wf, bf, k, nthreads=cores)
+        t += time.perf_counter() - t0
+        passes += 1
+        rows += Xf.shape[0]
+    return {"value": rows / t, "unit": "rows/s", "cores": cores, "kind": "port",
+            "sample": f"{passes} passes over the same {Xf.shape[0]}-row batch (full F and d, fp32 upcast "
+                      f"inputs), {t:.1f} s; oracle/stk_oracle_cpu.c, the reference streamtopk_cpu.cpp restated"}
+
+
+def copy_calibration(nbytes, steps):
+    """Plain elementwise copy of `nbytes` fp32 bytes (torch's vectorised
+    elementwise kernel: reads nbytes, writes nbytes), timed with HIP events.
+    Run under `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE` it gives the factor
+    that turns those counters into HBM bytes on this part."""
+    import torch
+    dev = torch.device("cuda:0")
+    n = nbytes // 4
+    src = torch.randn(n, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        torch.mul(src, 1.0, out=dst)
+    e1.record()
+    torch.cuda.synchronize()
+    us = 1e3 * e0.elapsed_time(e1) / steps
+    print(json.dumps({"copy_calibration": {"read_bytes": 4 * n, "write_bytes": 4 * n, "avg_us": round(us, 2),
+                                           "GBps_rw": round(8 * n / (us * 1e-6) / 1e9, 1)}}), flush=True)
+
+
+def traffic_from_profile(workload):
+    """HBM bytes per main_kernel launch, as recorded by the calibrated PMC
+    summary profiles/main_kernel_<workload>_hbm_traffic.md (a line
+    `traffic_bytes_per_launch: N`), or None when no such summary exists."""
+    path = os.path.join(ROOT, "profiles", f"main_kernel_{workload}_hbm_traffic.md")
+    try:
+        with open(path) as fh:
+            for line in fh:
+                line = line.strip().strip("`")
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        return None
+    return None
 
 
 def main():
@@ -82,6 +119,8 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="BYTES",
+                    help="only run the PMC calibration copy of BYTES bytes, --steps times")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -90,6 +129,10 @@ def main():
               "the encoder would shard F across GPUs with one small all-gather of (B, k) candidates, "
               "which is not built here.", file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_calib:
+        copy_calibration(args.copy_calib, args.steps)
+        return
 
     import torch
     from streamtopk_sae import _lib, make_inputs, topk_sae_cuda_approx, topk_sae_cuda_exact
@@ -157,7 +200,7 @@ def main():
         roof = {"bound": "mfma", "achieved": round(tflops_main, 2), "peak": MFMA_PEAK_TFLOPS[dtn],
                 "unit": "TFLOP/s", "frac": round(tflops_main / MFMA_PEAK_TFLOPS[dtn], 4)}
     roof["kernel"] = main_name
-    roof["traffic"] = None
+    roof["traffic"] = traffic_from_profile(args.workload)
     roof["alg_bytes_per_launch"] = alg_main
     roof["avg_launch_us"] = round(main_us, 2)
 
