@@ -73,25 +73,29 @@ def _device_checks(X, W_enc, b_enc, need_w_device=True):
         raise RuntimeError("b_enc F-dim mismatch")
 
 
-def topk_sae_cpu(X, W_enc, b_enc, k):
-    """CPU streaming top-k SAE forward (fp32; fp16/bf16 inputs are upcast).
+def _contiguity_checks(X, W_enc, b_enc):
+    # streamtopk_exact.cu:800-802 / streamtopk_approx.cu:243-245
+    if not X.is_contiguous():
+        raise RuntimeError("X must be contiguous")
+    if not W_enc.is_contiguous():
+        raise RuntimeError("W_enc must be contiguous")
+    if not b_enc.is_contiguous():
+        raise RuntimeError("b_enc must be contiguous")
 
-    Returns values (B, k) fp32 and indices (B, k) int32 on the CPU.
-    """
+
+def cpu_forward(X, W_enc, b_enc, k):
+    """The native CPU forward (streamtopk_cpu.cpp:81-125): fp32 contiguous CPU
+    tensors in, (V fp32 (B,k), I int32 (B,k)) out, rows sorted descending."""
     lib = _lib.load()
-    if X.dtype != torch.float32:
-        X = X.float()
-        W_enc = W_enc.float()
-    if b_enc.dtype != torch.float32:
-        b_enc = b_enc.float()
-    X = X.contiguous()
-    W_enc = W_enc.contiguous()
-    b_enc = b_enc.contiguous()
-    # streamtopk_cpu.cpp:87-99
+    # streamtopk_cpu.cpp:87-99 (plus a device check: the reference would read a
+    # device pointer on the host)
+    _contiguity_checks(X, W_enc, b_enc)
     if X.dtype != torch.float32:
         raise RuntimeError("X must be fp32")
     if W_enc.dtype != torch.float32:
         raise RuntimeError("W_enc must be fp32")
+    if b_enc.dtype != torch.float32:
+        raise RuntimeError("b_enc must be fp32")
     if X.is_cuda or W_enc.is_cuda or b_enc.is_cuda:
         raise RuntimeError("topk_sae_cpu expects CPU tensors")
     if W_enc.shape[1] != X.shape[1]:
@@ -108,26 +112,35 @@ def topk_sae_cpu(X, W_enc, b_enc, k):
     return V, I
 
 
-def _prepare_device(X, W_enc, b_enc):
+def topk_sae_cpu(X, W_enc, b_enc, k):
+    """CPU streaming top-k SAE forward (fp32; fp16/bf16 inputs are upcast).
+
+    Returns values (B, k) fp32 and indices (B, k) int32 on the CPU.
+    """
+    _lib.load()
+    if X.dtype != torch.float32:
+        X = X.float()
+        W_enc = W_enc.float()
     if b_enc.dtype != torch.float32:
         b_enc = b_enc.float()
-    X = X.contiguous()
-    W_enc = W_enc.contiguous()
-    b_enc = b_enc.contiguous()
+    return cpu_forward(X.contiguous(), W_enc.contiguous(), b_enc.contiguous(), k)
+
+
+def _device_inputs(X, W_enc, b_enc):
+    """Native-side checks, then the zero-padding of d to whole 128-byte steps
+    (32 fp32 or 64 fp16/bf16 elements) and 16-byte alignment."""
+    _contiguity_checks(X, W_enc, b_enc)
     _device_checks(X, W_enc, b_enc)
-    # the kernels stream 128-byte d-steps: 32 fp32 or 64 fp16/bf16 elements
     multiple = 32 if X.dtype == torch.float32 else 64
     X, W_enc = _pad_d(X, W_enc, multiple)
     return _aligned(X), _aligned(W_enc), b_enc
 
 
-def topk_sae_cuda_exact(X, W_enc, b_enc, k):
-    """Exact streaming top-k SAE forward on the GPU (fp16, bf16, fp32; b_enc fp32).
-
-    Returns values (B, k) fp32 and indices (B, k) int32 on X's device.
-    """
+def exact_forward(X, W_enc, b_enc, k):
+    """The native exact forward (streamtopk_exact.cu:788-833): contiguous device
+    tensors, fp32 b_enc; returns (V fp32 (B,k), I int32 (B,k))."""
     lib = _lib.load()
-    X, W_enc, b_enc = _prepare_device(X, W_enc, b_enc)
+    X, W_enc, b_enc = _device_inputs(X, W_enc, b_enc)
     B, d = X.shape
     F = W_enc.shape[0]
     dt = _DTYPES[X.dtype]
@@ -144,30 +157,41 @@ def topk_sae_cuda_exact(X, W_enc, b_enc, k):
     return V, I
 
 
-def topk_sae_cuda_approx(X, W_enc, b_enc, k, c, candidate_buffer=None):
-    """Approximate streaming top-k SAE forward: top-c per 128-latent group, then
-    top-k of the union.  c must be in {16, 32, 64, 128} and >= k.
+def topk_sae_cuda_exact(X, W_enc, b_enc, k):
+    """Exact streaming top-k SAE forward on the GPU (fp16, bf16, fp32; b_enc fp32).
 
-    If `candidate_buffer` (fp32, shape (B, ceil(F/128), c)) is given it is
-    filled with each group's top-c values, descending, padded with -FLT_MAX.
-    Returns values (B, k) fp32 and indices (B, k) int32.
+    Returns values (B, k) fp32 and indices (B, k) int32 on X's device.
     """
+    _lib.load()
+    if b_enc.dtype != torch.float32:
+        b_enc = b_enc.float()
+    return exact_forward(X.contiguous(), W_enc.contiguous(), b_enc.contiguous(), k)
+
+
+def approx_forward(X, W_enc, b_enc, k, c, candidate_buffer=None, candidates=False):
+    """The native approximate forward (streamtopk_approx.cu:234-291) with the
+    final top-k done on the device.  Returns (V, I, cand_vals, cand_idxs); the
+    candidate tensors, shape (B, ceil(F/128), c), are None unless
+    `candidates` is set or a `candidate_buffer` is given."""
     lib = _lib.load()
-    X, W_enc, b_enc = _prepare_device(X, W_enc, b_enc)
+    X, W_enc, b_enc = _device_inputs(X, W_enc, b_enc)
     B, d = X.shape
     F = W_enc.shape[0]
     dt = _DTYPES[X.dtype]
     nt = (F + 127) // 128
     with torch.cuda.device(X.device):
-        with_cand = candidate_buffer is not None
+        with_cand = candidate_buffer is not None or candidates
         cand_vals = cand_idxs = None
         if with_cand:
-            cb = candidate_buffer
-            if cb.dim() != 3 or tuple(cb.shape) != (B, nt, c):
-                raise RuntimeError("candidate_buffer shape mismatch")
-            if cb.dtype != torch.float32 or cb.device != X.device or not cb.is_contiguous():
-                raise RuntimeError("candidate_buffer must be a contiguous fp32 tensor on X's device")
-            cand_vals = cb
+            if candidate_buffer is not None:
+                cb = candidate_buffer
+                if cb.dim() != 3 or tuple(cb.shape) != (B, nt, c):
+                    raise RuntimeError("candidate_buffer shape mismatch")
+                if cb.dtype != torch.float32 or cb.device != X.device or not cb.is_contiguous():
+                    raise RuntimeError("candidate_buffer must be a contiguous fp32 tensor on X's device")
+                cand_vals = cb
+            else:
+                cand_vals = torch.empty((B, nt, c), dtype=torch.float32, device=X.device)
             cand_idxs = torch.empty((B, nt, c), dtype=torch.int32, device=X.device)
         nbytes = ctypes.c_size_t(0)
         _lib.check(lib.stk_approx_workspace_bytes(B, d, F, k, c, dt, int(with_cand),
@@ -180,4 +204,20 @@ def topk_sae_cuda_approx(X, W_enc, b_enc, k, c, candidate_buffer=None):
                                     B, d, F, k, c, dt, _ptr(cand_vals), _ptr(cand_idxs),
                                     _ptr(ws), ws.numel(), ctypes.c_void_p(stream))
         _lib.check(rc)
+    return V, I, cand_vals, cand_idxs
+
+
+def topk_sae_cuda_approx(X, W_enc, b_enc, k, c, candidate_buffer=None):
+    """Approximate streaming top-k SAE forward: top-c per 128-latent group, then
+    top-k of the union.  c must be in {16, 32, 64, 128} and >= k.
+
+    If `candidate_buffer` (fp32, shape (B, ceil(F/128), c)) is given it is
+    filled with each group's top-c values, descending, padded with -FLT_MAX.
+    Returns values (B, k) fp32 and indices (B, k) int32.
+    """
+    _lib.load()
+    if b_enc.dtype != torch.float32:
+        b_enc = b_enc.float()
+    V, I, _, _ = approx_forward(X.contiguous(), W_enc.contiguous(), b_enc.contiguous(), k, c,
+                                candidate_buffer)
     return V, I

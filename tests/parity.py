@@ -23,7 +23,8 @@ def check_against_scores(V, I, S, k, rtol, name=""):
     B, F = S.shape
     assert V.shape == (B, k) and I.shape == (B, k), f"{name}: shape {V.shape} {I.shape}"
     assert np.all((I >= 0) & (I < F)), f"{name}: index out of range"
-    ref = -np.sort(-S, axis=1)[:, :k]
+    part = np.partition(S, F - k, axis=1)[:, F - k:] if k < F else S
+    ref = -np.sort(-part, axis=1)
     scale = np.maximum(np.abs(ref), 1.0)
     err = np.abs(V - ref) / scale
     assert np.all(err <= rtol), f"{name}: sorted values differ, max rel err {err.max():.3g}"
@@ -34,11 +35,12 @@ def check_against_scores(V, I, S, k, rtol, name=""):
     ties = 0
     for i in range(B):
         assert len(set(I[i].tolist())) == k, f"{name}: duplicate index in row {i}"
-        order = np.lexsort((np.arange(F), -S[i]))
-        want = set(order[:k].tolist())
+        kth = ref[i, k - 1]
+        above = np.nonzero(S[i] > kth)[0]
+        level = np.nonzero(S[i] == kth)[0][:k - above.size]   # lower index first among equals
+        want = set(above.tolist()) | set(level.tolist())
         diff = set(I[i].tolist()) ^ want
         if diff:
-            kth = ref[i, k - 1]
             for f in diff:
                 assert abs(S[i, f] - kth) <= rtol * max(abs(kth), 1.0), (
                     f"{name}: row {i} index {f} (score {S[i, f]!r}) differs beyond a near-tie "

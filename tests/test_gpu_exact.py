@@ -199,3 +199,53 @@ def test_exact_known_answers(cuda_dev, dtype_name):
         V, I = topk_sae_cuda_exact(Xt, Wt, bt, k)
         assert np.array_equal(V.cpu().numpy(), Vk), f"{dtype_name} {X.shape} {W.shape} k={k}"
         assert np.array_equal(I.cpu().numpy(), Ik), f"{dtype_name} {X.shape} {W.shape} k={k}"
+
+
+# BASELINE config 2 (headline) at full size: B=128 d=2048 F=262144 k=64, and
+# its edge cases (F=262143, k=1, all-zero X, one b_enc entry at +1e4).
+C2 = dict(B=128, d=2048, F=262144, k=64)
+
+
+@pytest.mark.parametrize("dtype_name", ["bf16", "fp16", "fp32"])
+def test_exact_headline_config(cuda_dev, dtype_name):
+    print(f"case headline {dtype_name}", flush=True)
+    X, W, b = make_inputs(C2["B"], C2["d"], C2["F"], DT[dtype_name], seed=0, device=cuda_dev)
+    _run_check(X, W, b, C2["k"], dtype_name, scores="torch64", name=f"headline/{dtype_name}")
+
+
+def test_exact_headline_F_not_multiple_of_tile(cuda_dev):
+    print("case headline F=262143", flush=True)
+    X, W, b = make_inputs(C2["B"], C2["d"], C2["F"] - 1, torch.bfloat16, seed=1, device=cuda_dev)
+    V, I = _run_check(X, W, b, C2["k"], "bf16", scores="torch64", name="headline/F=262143")
+    assert int(I.max()) < C2["F"] - 1 and int(I.min()) >= 0
+
+
+def test_exact_headline_k1(cuda_dev):
+    print("case headline k=1", flush=True)
+    X, W, b = make_inputs(C2["B"], C2["d"], C2["F"], torch.bfloat16, seed=2, device=cuda_dev)
+    V, I = _run_check(X, W, b, 1, "bf16", scores="torch64", name="headline/k=1")
+    # k=1 is the row argmax: its value must be the row maximum of the float64 scores
+    Smax = (X.double() @ W.double().T + b.double()).max(dim=1).values.float()
+    assert torch.allclose(V[:, 0], Smax, rtol=2e-3, atol=2e-3)
+
+
+def test_exact_headline_zero_X(cuda_dev):
+    """All-zero X: every row's result is the top-k of b_enc, bit-exact, lower index first."""
+    print("case headline zero X", flush=True)
+    _, W, b = make_inputs(C2["B"], C2["d"], C2["F"], torch.bfloat16, seed=3, device=cuda_dev)
+    X = torch.zeros(C2["B"], C2["d"], dtype=torch.bfloat16, device=cuda_dev)
+    V, I = topk_sae_cuda_exact(X, W, b, C2["k"])
+    bn = b.cpu().numpy()
+    order = np.lexsort((np.arange(bn.size), -bn.astype(np.float64)))[:C2["k"]]
+    assert np.array_equal(I.cpu().numpy(), np.broadcast_to(order.astype(np.int32), (C2["B"], C2["k"])))
+    assert np.array_equal(V.cpu().numpy(), np.broadcast_to(bn[order], (C2["B"], C2["k"])))
+
+
+def test_exact_headline_large_bias(cuda_dev):
+    """One b_enc entry at +1e4: that latent is rank 0 of every row."""
+    print("case headline large bias", flush=True)
+    X, W, b = make_inputs(C2["B"], C2["d"], C2["F"], torch.bfloat16, seed=4, device=cuda_dev)
+    j = 123457
+    b[j] = 1e4
+    V, I = _run_check(X, W, b, C2["k"], "bf16", scores="torch64", name="headline/bias")
+    assert torch.all(I[:, 0] == j)
