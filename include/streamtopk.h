@@ -91,13 +91,15 @@ int stk_cpu_forward(const float* X, const float* W, const float* b, float* V, in
 
 /* Per-kernel timing (no counterpart in the reference; used by bench.py).
  * While enabled, every device entry point called on this thread records a HIP
- * event pair on its stream around each kernel it launches.  Enabling (on=1)
+ * event pair on its stream around the kernels it launches: every kernel for
+ * on=1, only the streaming kernels (main_kernel, group_kernel) for on=2, so
+ * that timing a loop adds no events between the other kernels.  Enabling
  * discards earlier records; on=0 stops recording and frees the events. */
 int stk_profile_enable(int on);
 
 /* Total milliseconds and number of launches recorded for `kernel`
- * ("sample_kernel", "seed_kernel", "main_kernel", "merge_kernel",
- * "group_kernel", "cand_kernel") since stk_profile_enable(1).  Waits for the
+ * ("sample_kernel", "thr_kernel", "main_kernel", "merge_kernel",
+ * "group_kernel", "cand_kernel") since profiling was enabled.  Waits for the
  * recorded events to complete. */
 int stk_profile_read(const char* kernel, double* total_ms, int64_t* launches);
 

@@ -46,7 +46,7 @@ struct ProfRec {
     const char* name;
     hipEvent_t a, b;
 };
-static thread_local bool g_prof = false;
+static thread_local int g_prof = 0;   // 0 off, 1 every kernel, 2 streaming kernels only
 static thread_local std::vector<ProfRec> g_recs;
 static thread_local std::vector<hipEvent_t> g_pool;
 
@@ -65,6 +65,7 @@ static hipEvent_t prof_event()
 static int prof_begin(const char* name, hipStream_t st)
 {
     if (!g_prof) return -1;
+    if (g_prof == 2 && std::strcmp(name, "main_kernel") != 0 && std::strcmp(name, "group_kernel") != 0) return -1;
     ProfRec r{name, prof_event(), prof_event()};
     if (!r.a || !r.b) return -1;
     (void)hipEventRecord(r.a, st);
@@ -113,7 +114,8 @@ struct ExactPlan {
     int nwg;
     bool sample;
     int samp_log2;
-    size_t off_seed, off_thr, off_P, off_keys, off_cnt, total;
+    int64_t list_cap;
+    size_t off_thr, off_P, off_list, off_lcnt, total;
 };
 
 static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int dtype, int ncu)
@@ -141,17 +143,16 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
         // kSampleBlocks blocks of kSampleBlock consecutive latents, 1 << samp_log2 apart
         p.samp_log2 = ilog2_floor(F / kSampleBlocks);
     }
+    p.list_cap = (p.sample ? kSampleTarget : 0) + (int64_t)p.nwg * p.cap;
     size_t off = 0;
-    p.off_seed = off;
-    if (p.sample) off = align256(off + (size_t)B * k * 8);
     p.off_thr = off;
-    if (p.sample) off = align256(off + (size_t)B * 8);
+    off = align256(off + (size_t)B * 8);
     p.off_P = off;
     if (p.sample) off = align256(off + (size_t)B * kSampleTarget * 4);
-    p.off_keys = off;
-    off = align256(off + (size_t)B * p.nwg * p.cap * 8);
-    p.off_cnt = off;
-    off = align256(off + (size_t)B * p.nwg * 4);
+    p.off_list = off;
+    off = align256(off + (size_t)B * p.list_cap * 8);
+    p.off_lcnt = off;
+    off = align256(off + (size_t)B * 4);
     p.total = off;
     return p;
 }
@@ -198,49 +199,49 @@ static int validate_exact(int64_t B, int64_t d, int64_t F, int64_t k, int dtype)
     return check_shape_common(B, d, F, dtype);
 }
 
-// Runs sample -> seed -> main -> merge on `st`.
+// Runs sample -> thr -> main -> merge on `st`.
 static int run_exact(const ExactPlan& p, const void* X, const void* W, const float* b, float* V, int32_t* I,
                      int64_t B, int64_t d, int64_t F, int64_t k, int dtype, unsigned char* ws, hipStream_t st)
 {
     const int dt = dtype;   // STK_DTYPE_* and DT_* share values
     hipError_t e;
-    uint64_t* seed = (uint64_t*)(ws + p.off_seed);
     uint64_t* thr = (uint64_t*)(ws + p.off_thr);
+    uint64_t* list_keys = (uint64_t*)(ws + p.off_list);
+    int32_t* list_cnt = (int32_t*)(ws + p.off_lcnt);
+    float* P = p.sample ? (float*)(ws + p.off_P) : nullptr;
     if (p.sample) {
         SampleArgs sa;
         sa.X = X; sa.W = W; sa.bias = b; sa.B = B; sa.d = d;
         sa.samp_log2 = p.samp_log2;
-        sa.P = (float*)(ws + p.off_P);
+        sa.P = P;
         int pi = prof_begin("sample_kernel", st);
         e = launch_sample(dt, sa, dim3((unsigned)(kSampleTarget / 32), (unsigned)cdiv(B, 32)), st);
         prof_end(pi, st);
         if (e != hipSuccess) return hip_fail(e, "sample_kernel launch");
-        SeedArgs sd;
-        sd.P = sa.P;
-        sd.samp_log2 = p.samp_log2; sd.k = (int)k;
-        sd.seed_keys = seed; sd.thr = thr;
-        pi = prof_begin("seed_kernel", st);
-        e = launch_seed(sd, B, st);
-        prof_end(pi, st);
-        if (e != hipSuccess) return hip_fail(e, "seed_kernel launch");
     }
+    ThrArgs ta;
+    ta.P = P;
+    ta.samp_log2 = p.samp_log2; ta.k = (int)k;
+    ta.thr = thr; ta.list_keys = list_keys; ta.list_cnt = list_cnt; ta.list_cap = p.list_cap;
+    int pt = prof_begin("thr_kernel", st);
+    e = launch_thr(ta, B, st);
+    prof_end(pt, st);
+    if (e != hipSuccess) return hip_fail(e, "thr_kernel launch");
     MainArgs ma;
     ma.X = X; ma.W = W; ma.bias = b; ma.B = B; ma.d = d; ma.F = F;
     ma.k = (int)k; ma.cap = p.cap;
-    ma.num_tiles = p.num_tiles; ma.tiles_per_wg = p.tpw; ma.nwg = p.nwg;
-    ma.thr0 = p.sample ? thr : nullptr;
+    ma.num_tiles = p.num_tiles; ma.tiles_per_wg = p.tpw;
+    ma.thr0 = thr;
     ma.sampled = p.sample ? 1 : 0;
     ma.samp_log2 = p.samp_log2;
-    ma.out_keys = (uint64_t*)(ws + p.off_keys);
-    ma.out_cnt = (int32_t*)(ws + p.off_cnt);
+    ma.list_keys = list_keys; ma.list_cnt = list_cnt; ma.list_cap = p.list_cap;
     int pm = prof_begin("main_kernel", st);
     e = launch_main(dt, p.NB, ma, dim3((unsigned)p.nwg, (unsigned)p.nbc), st);
     prof_end(pm, st);
     if (e != hipSuccess) return hip_fail(e, "main_kernel launch");
     MergeArgs mg;
-    mg.seed_keys = p.sample ? seed : nullptr;
-    mg.seg_keys = ma.out_keys; mg.seg_cnt = ma.out_cnt;
-    mg.nseg = p.nwg; mg.cap = p.cap; mg.k = (int)k;
+    mg.list_keys = list_keys; mg.list_cnt = list_cnt; mg.list_cap = p.list_cap;
+    mg.k = (int)k;
     mg.V = V; mg.I = I;
     pm = prof_begin("merge_kernel", st);
     e = launch_merge(mg, B, st);
@@ -393,8 +394,9 @@ int stk_approx_forward(const void* X, const void* W, const float* b, float* V, i
 int stk_profile_enable(int on)
 {
     clear_error();
+    if (on < 0 || on > 2) return set_error(STK_E_INVALID, "stk_profile_enable: mode must be 0, 1 or 2");
     prof_release();
-    g_prof = on != 0;
+    g_prof = on;
     if (!g_prof) {
         for (hipEvent_t e : g_pool) (void)hipEventDestroy(e);
         g_pool.clear();

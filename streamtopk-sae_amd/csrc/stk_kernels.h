@@ -36,12 +36,13 @@ struct MainArgs {
     int64_t B, d, F;
     int k, cap;
     int64_t num_tiles, tiles_per_wg;
-    int nwg;
     const uint64_t* thr0;        // per-row starting threshold keys, or null
     int sampled;                 // non-zero: the sampled latents (is_sampled) were
-    int samp_log2;               //   scored by the sample pass and are skipped here
-    uint64_t* out_keys;          // [B][nwg][cap]
-    int32_t* out_cnt;            // [B][nwg]
+    int samp_log2;               //   scored by sample_kernel and are skipped here
+    uint64_t* list_keys;         // [B][list_cap]: every workgroup's final queue, appended
+    int32_t* list_cnt;           // [B] keys in each row's list (set by thr_kernel)
+    int64_t list_cap;            // kSampleTarget + nwg * cap: room for the sampled keys
+                                 //   and every workgroup's full queue
 };
 
 struct SampleArgs {
@@ -53,19 +54,20 @@ struct SampleArgs {
     float* P;                    // [B][kSampleTarget] scores of the sampled latents
 };
 
-struct SeedArgs {
-    const float* P;
+struct ThrArgs {
+    const float* P;              // sampled scores, or null (no sample: threshold 0)
     int samp_log2, k;
-    uint64_t* seed_keys;         // [B][k], descending
-    uint64_t* thr;               // [B]
+    uint64_t* thr;               // [B] row threshold keys
+    uint64_t* list_keys;         // [B][list_cap]: receives the sampled keys >= thr
+    int32_t* list_cnt;           // [B] set to the number of those keys
+    int64_t list_cap;
 };
 
 struct MergeArgs {
-    const uint64_t* seed_keys;   // [B][k] or null
-    const uint64_t* seg_keys;    // [B][nseg][cap]
-    const int32_t* seg_cnt;      // [B][nseg]
-    int64_t nseg;
-    int cap, k;
+    const uint64_t* list_keys;   // [B][list_cap]
+    const int32_t* list_cnt;     // [B]
+    int64_t list_cap;
+    int k;
     float* V;
     int32_t* I;
 };
@@ -95,7 +97,7 @@ size_t group_lds_bytes(int NB);
 
 hipError_t launch_main(int dt, int NB, const MainArgs& a, dim3 grid, hipStream_t st);
 hipError_t launch_sample(int dt, const SampleArgs& a, dim3 grid, hipStream_t st);
-hipError_t launch_seed(const SeedArgs& a, int64_t rows, hipStream_t st);
+hipError_t launch_thr(const ThrArgs& a, int64_t rows, hipStream_t st);
 hipError_t launch_merge(const MergeArgs& a, int64_t rows, hipStream_t st);
 hipError_t launch_group(int dt, int NB, const GroupArgs& a, dim3 grid, hipStream_t st);
 hipError_t launch_cand(const CandArgs& a, int64_t rows, hipStream_t st);

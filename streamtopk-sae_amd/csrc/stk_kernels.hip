@@ -1,14 +1,19 @@
-// stk_kernels.hip -- gfx950 kernels of the streaming fused top-k SAE encoder.
+// stk_kernels.hip -- the exact streaming top-k encoder on gfx950.
 //
-//   sample_kernel  : fp32 scores of a strided sample of latents (split over d),
-//                    the seed of the per-row thresholds.
-//   seed_kernel    : per row, the exact top-k of the sample -> seed keys and
-//                    the row threshold (the seed's k-th key).
+//   sample_kernel  : fp32 scores of kSampleTarget sampled latents (32 blocks of
+//                    128 consecutive latents spread over F) for every row.
+//   thr_kernel     : per row, a threshold key that at least k sampled keys
+//                    reach (the k-th largest of the per-thread maxima), hence a
+//                    lower bound of the row's k-th key; the sampled keys that
+//                    reach it open the row's candidate list.
 //   main_kernel    : streams W once; MFMA scores for 256 latents x up to 128
-//                    rows per tile; scores above the row threshold go to a
+//                    rows per tile (the sampled latents are skipped: each latent
+//                    is scored by exactly one kernel); scores not below the
+//                    row threshold go to a
 //                    per-row LDS queue that is rank-compacted to its top-k
-//                    whenever it fills.  Emits each workgroup's queue.
-//   merge_kernel   : per row, top-k of the seed plus every workgroup queue.
+//                    whenever it fills.  Appends each workgroup's final queue to
+//                    a dense per-row candidate list.
+//   merge_kernel   : per row, top-k of its candidate list.
 //
 // The reference's pass 1 / pass 2 split (streamtopk_exact.cu:58-187 tile
 // kernel, :429-499 merge kernel) maps to main_kernel / merge_kernel; its
@@ -171,16 +176,19 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
         }
     });
 
-    // ---- emit this workgroup's queues ----
+    // ---- append this workgroup's queues to the rows' candidate lists ----
+    __syncthreads();
+    int* lbase = (int*)thr;   // the thresholds are no longer needed
+    for (int i = tid; i < BT; i += kMainThreads) {
+        const int c = (b0 + i < B) ? (cnt[i] < cap ? cnt[i] : cap) : 0;
+        cnt[i] = c;
+        lbase[i] = c ? atomicAdd(&a.list_cnt[b0 + i], c) : 0;
+    }
     __syncthreads();
     for (int idx = tid; idx < BT * cap; idx += kMainThreads) {
         const int row = idx / cap, e = idx - row * cap;
-        if (b0 + row < B) {
-            const int c = cnt[row] < cap ? cnt[row] : cap;
-            const size_t seg = (size_t)(b0 + row) * a.nwg + blockIdx.x;
-            if (e < c) a.out_keys[seg * cap + e] = q[(size_t)row * cap + e];
-            if (e == 0) a.out_cnt[seg] = c;
-        }
+        if (e < cnt[row])
+            a.list_keys[(size_t)(b0 + row) * a.list_cap + lbase[row] + e] = q[(size_t)row * cap + e];
     }
 }
 
@@ -202,11 +210,21 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a)
     const int64_t ib = (int64_t)blockIdx.x * 32;
     const int64_t jb = (int64_t)blockIdx.y * 32;
     const int64_t d = a.d;
-    const int64_t nds = (d + DS - 1) / DS;
+    const int64_t nds = d / DS;   // d is a whole number of steps (checked on the host)
+
+    // the bias of this lane's output latents, fetched first: stores to P could
+    // alias it, so it must not be read after them
+    float bias_r[16];
+    if (wave == 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            bias_r[r] = a.bias[sample_latent(ib + (r >> 2) * 8 + h * 4 + (r & 3), a.samp_log2)];
+    }
 
     const unsigned char* wp = (const unsigned char*)a.W + sample_latent(ib + jl, a.samp_log2) * d * ES + h * 64;
     const int64_t j = jb + jl;
     const bool jok = j < a.B;
+    // rows past B read row 0; their sums are never stored
     const unsigned char* xp = (const unsigned char*)a.X + (jok ? j : 0) * d * ES + h * 64;
 
     f32x16 acc;
@@ -217,12 +235,15 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a)
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int64_t s = s0 + t * kWaves;
+            const int64_t sc = s < nds ? s : nds - 1;   // in bounds; zeroed below
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int64_t e0 = s * DS + h * (DS / 2) + q * (DS / 8);
-                const bool ok = s < nds && e0 < d;
-                wq[t][q] = ok ? *(const u32x4*)(wp + s * kStepBytes + q * 16) : u32x4{0u, 0u, 0u, 0u};
-                xq[t][q] = (ok && jok) ? *(const u32x4*)(xp + s * kStepBytes + q * 16) : u32x4{0u, 0u, 0u, 0u};
+                wq[t][q] = *(const u32x4*)(wp + sc * kStepBytes + q * 16);
+                xq[t][q] = *(const u32x4*)(xp + sc * kStepBytes + q * 16);
+            }
+            if (s >= nds) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) wq[t][q] = u32x4{0u, 0u, 0u, 0u};
             }
         }
 #pragma unroll
@@ -241,7 +262,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a)
         for (int r = 0; r < 16; ++r) {
             const int64_t ii = ib + (r >> 2) * 8 + h * 4 + (r & 3);
             const float s = ((acc[r] + red[0][r][lane]) + red[1][r][lane]) + red[2][r][lane];
-            prow[ii] = s + a.bias[sample_latent(ii, a.samp_log2)];
+            prow[ii] = s + bias_r[r];
         }
     }
 }
@@ -249,99 +270,99 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a)
 // ---------------------------------------------------------------------------
 // Selection kernels (one workgroup per row).
 // ---------------------------------------------------------------------------
-__device__ inline void append_key(SelShared& S, uint64_t key, bool& stalled)
-{
-    const int pos = atomicAdd(&S.cnt, 1);
-    if (pos < kSelCap)
-        S.buf[pos] = key;
-    else
-        stalled = true;
-}
-
-// Per row: exact top-k of the sampled scores -> seed keys and row threshold.
-__global__ __launch_bounds__(kThreads) void seed_kernel(SeedArgs a)
+// Per row: the threshold key main_kernel starts from and the head of the
+// row's candidate list.  At least k sampled keys are >= the threshold
+// (kth_of_maxima), so it never exceeds the row's final k-th key; the sampled
+// keys that reach it are written to the list, since main_kernel skips the
+// sampled latents.
+__global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
 {
     constexpr int kItems = kSampleTarget / kThreads;
     __shared__ SelShared S;
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
-    const int k = a.k;
+    if (a.P == nullptr) {
+        if (tid == 0) { a.thr[row] = 0; a.list_cnt[row] = 0; }
+        return;
+    }
     const float* prow = a.P + row * kSampleTarget;
+    float v[kItems];
+#pragma unroll
+    for (int t = 0; t < kItems; ++t) v[t] = prow[tid + t * kThreads];
     uint64_t key[kItems];
     uint64_t m = 0;
 #pragma unroll
     for (int t = 0; t < kItems; ++t) {
-        const int64_t i = tid + (int64_t)t * kThreads;
-        key[t] = make_key(prow[i], sample_latent(i, a.samp_log2));
+        key[t] = make_key(v[t], sample_latent(tid + t * kThreads, a.samp_log2));
         m = key[t] > m ? key[t] : m;
     }
     if (tid == 0) S.cnt = 0;
-    const uint64_t T = kth_of_maxima(S, m, k, tid);
-    bool stalled = false;
+    const uint64_t T = kth_of_maxima(S, m, a.k, tid);
+    uint32_t pass = 0;
+#pragma unroll
+    for (int t = 0; t < kItems; ++t) pass |= (key[t] >= T) ? (1u << t) : 0u;
+    const int base = pass ? atomicAdd(&S.cnt, __builtin_popcount(pass)) : 0;
+    uint64_t* out = a.list_keys + row * a.list_cap;
 #pragma unroll
     for (int t = 0; t < kItems; ++t)
-        if (key[t] != 0 && key[t] >= T) append_key(S, key[t], stalled);
-    emit_topk(S, k, tid, [&](int r, uint64_t kk) {
-        a.seed_keys[row * k + r] = kk;
-        if (r == k - 1) a.thr[row] = kk;
-    });
+        if (pass >> t & 1u) out[base + __builtin_popcount(pass & ((1u << t) - 1u))] = key[t];
+    __syncthreads();
+    if (tid == 0) {
+        a.thr[row] = T;
+        a.list_cnt[row] = S.cnt;
+    }
 }
 
-// Per row: top-k of the seed keys plus every main_kernel workgroup queue.
+// Per row: top-k of the candidate list, read in chunks of kPer keys per
+// thread.  Each chunk is filtered against the larger of its own k-th of the
+// per-thread maxima and the k-th key of the last compaction.
 __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
 {
+    constexpr int kPer = 16;
     __shared__ SelShared S;
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
     const int k = a.k;
-    // pass 1: each thread's largest key (seed entry tid, segments tid + 256 j)
-    uint64_t m = 0;
-    if (a.seed_keys != nullptr && tid < k) m = a.seed_keys[row * k + tid];
-    for (int64_t seg = tid; seg < a.nseg; seg += kThreads) {
-        const int64_t sid = row * a.nseg + seg;
-        const int c = a.seg_cnt[sid];
-        const uint64_t* keys = a.seg_keys + sid * a.cap;
-        for (int e0 = 0; e0 < c; e0 += 8) {
-            uint64_t v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = (e0 + u < c) ? keys[e0 + u] : 0ull;
-#pragma unroll
-            for (int u = 0; u < 8; ++u) m = v[u] > m ? v[u] : m;
-        }
-    }
+    const int64_t n = a.list_cnt[row];
+    const uint64_t* keys = a.list_keys + row * a.list_cap;
     if (tid == 0) S.cnt = 0;
-    const uint64_t T = kth_of_maxima(S, m, k, tid);
-    // pass 2: append every key >= the running threshold; compact when full
-    bool seed_done = !(a.seed_keys != nullptr && tid < k);
-    int64_t seg = tid;
-    int e = 0;
-    for (;;) {
-        const uint64_t thr = S.thr > T ? S.thr : T;
-        bool stalled = false;
-        if (!seed_done) {
-            const uint64_t kk = a.seed_keys[row * k + tid];
-            if (kk >= thr) append_key(S, kk, stalled);
-            seed_done = !stalled;
+    uint64_t run = 0;
+    for (int64_t c0 = 0; c0 < n; c0 += (int64_t)kPer * kThreads) {
+        uint64_t v[kPer];
+        uint64_t m = 0;
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            const int64_t i = c0 + tid + (int64_t)u * kThreads;
+            v[u] = i < n ? keys[i] : 0ull;
         }
-        while (!stalled && seg < a.nseg) {
-            const int64_t sid = row * a.nseg + seg;
-            const int c = a.seg_cnt[sid];
-            const uint64_t* keys = a.seg_keys + sid * a.cap;
-            while (e < c) {
-                const uint64_t kk = keys[e];
-                if (kk >= thr) {
-                    append_key(S, kk, stalled);
-                    if (stalled) break;
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) m = v[u] > m ? v[u] : m;
+        const uint64_t T = kth_of_maxima(S, m, k, tid);
+        const uint64_t thr = T > run ? T : run;
+        uint32_t pend = 0;
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) pend |= (v[u] != 0 && v[u] >= thr) ? (1u << u) : 0u;
+        for (;;) {
+            bool stalled = false;
+#pragma unroll
+            for (int u = 0; u < kPer; ++u) {
+                if (pend >> u & 1u) {
+                    const int pos = atomicAdd(&S.cnt, 1);
+                    if (pos < kSelCap) {
+                        S.buf[pos] = v[u];
+                        pend &= ~(1u << u);
+                    } else {
+                        stalled = true;
+                    }
                 }
-                ++e;
             }
-            if (stalled) break;
-            seg += kThreads;
-            e = 0;
+            if (!__syncthreads_or(stalled)) break;
+            select_compact(S, kSelCap, k, tid);   // S.cnt = k, S.thr = k-th key
+            run = S.thr;
+#pragma unroll
+            for (int u = 0; u < kPer; ++u)
+                if ((pend >> u & 1u) && !(v[u] > run)) pend &= ~(1u << u);
         }
-        __syncthreads();
-        if (S.cnt >= kSelCap) select_compact(S, kSelCap, k, tid);
-        if (!__syncthreads_or(stalled)) break;
     }
     emit_topk(S, k, tid, [&](int r, uint64_t kk) {
         a.V[row * k + r] = key_value(kk);
@@ -389,9 +410,9 @@ hipError_t launch_sample(int dt, const SampleArgs& a, dim3 grid, hipStream_t st)
     return hipGetLastError();
 }
 
-hipError_t launch_seed(const SeedArgs& a, int64_t rows, hipStream_t st)
+hipError_t launch_thr(const ThrArgs& a, int64_t rows, hipStream_t st)
 {
-    hipLaunchKernelGGL(seed_kernel, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL(thr_kernel, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     return hipGetLastError();
 }
 
