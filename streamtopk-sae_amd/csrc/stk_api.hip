@@ -109,13 +109,14 @@ static int ilog2_floor(int64_t x) { int l = 0; while ((x >> (l + 1)) > 0) ++l; r
 // Exact-path plan
 // ---------------------------------------------------------------------------
 struct ExactPlan {
+    bool large;                  // mainl_kernel (B >= kLargeMinB) instead of main_kernel
     int NB, cap;
     int64_t nbc, num_tiles, tpw;
-    int nwg;
+    int nwg;                     // main_kernel: W ranges; mainl_kernel: nr (grid = nbc * nr)
     bool sample;
     int samp_log2;
-    int64_t list_cap;
-    size_t off_thr, off_P, off_list, off_lcnt, total;
+    int64_t list_cap, head_span;
+    size_t off_thr, off_P, off_list, off_lcnt, off_seg, total;
 };
 
 static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int dtype, int ncu)
@@ -123,19 +124,33 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
     ExactPlan p;
     (void)d;
     (void)dtype;
-    const int64_t bblocks = cdiv(B > 0 ? B : 1, 32);
-    const int64_t nb_max = (k > 64) ? 2 : 4;   // k=128 queues need the LDS of 64 rows
-    p.NB = (int)(bblocks < nb_max ? bblocks : nb_max);
-    if (p.NB == 3) p.NB = 4;
-    p.cap = (int)(k + 32);
-    if (p.cap & 1) ++p.cap;
-    p.nbc = cdiv(B, 32 * p.NB);
     p.num_tiles = cdiv(F, kTileLatents);
-    int64_t nwg = ncu / (p.nbc > 0 ? p.nbc : 1);
-    if (nwg < 1) nwg = 1;
-    if (nwg > p.num_tiles) nwg = p.num_tiles;
-    p.tpw = cdiv(p.num_tiles, nwg);
-    p.nwg = (int)cdiv(p.num_tiles, p.tpw);
+    p.large = B >= kLargeMinB;
+    if (p.large) {
+        // 256-row blocks; W ranges a multiple of 8 so each range's row blocks share an XCD
+        p.NB = kLargeRows / 32;
+        p.cap = (int)(k + 64 < 192 ? k + 64 : 192);
+        if (p.cap & 1) ++p.cap;
+        p.nbc = cdiv(B, kLargeRows);
+        int64_t nr = ncu / p.nbc;
+        if (nr < 1) nr = 1;
+        if (nr >= 8) nr &= ~(int64_t)7;
+        p.tpw = cdiv(p.num_tiles, nr);
+        p.nwg = (int)nr;
+    } else {
+        const int64_t bblocks = cdiv(B > 0 ? B : 1, 32);
+        const int64_t nb_max = (k > 64) ? 2 : 4;   // k=128 queues need the LDS of 64 rows
+        p.NB = (int)(bblocks < nb_max ? bblocks : nb_max);
+        if (p.NB == 3) p.NB = 4;
+        p.cap = (int)(k + 32);
+        if (p.cap & 1) ++p.cap;
+        p.nbc = cdiv(B, 32 * p.NB);
+        int64_t nwg = ncu / (p.nbc > 0 ? p.nbc : 1);
+        if (nwg < 1) nwg = 1;
+        if (nwg > p.num_tiles) nwg = p.num_tiles;
+        p.tpw = cdiv(p.num_tiles, nwg);
+        p.nwg = (int)cdiv(p.num_tiles, p.tpw);
+    }
 
     p.sample = F >= kSampleMinF;
     p.samp_log2 = 0;
@@ -143,7 +158,8 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
         // kSampleBlocks blocks of kSampleBlock consecutive latents, 1 << samp_log2 apart
         p.samp_log2 = ilog2_floor(F / kSampleBlocks);
     }
-    p.list_cap = (p.sample ? kSampleTarget : 0) + (int64_t)p.nwg * p.cap;
+    p.head_span = p.sample ? kSampleTarget : 0;
+    p.list_cap = p.head_span + (int64_t)p.nwg * p.cap;
     size_t off = 0;
     p.off_thr = off;
     off = align256(off + (size_t)B * 8);
@@ -153,6 +169,8 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
     off = align256(off + (size_t)B * p.list_cap * 8);
     p.off_lcnt = off;
     off = align256(off + (size_t)B * 4);
+    p.off_seg = off;
+    if (p.large) off = align256(off + (size_t)B * p.nwg * 4);
     p.total = off;
     return p;
 }
@@ -227,25 +245,45 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     e = launch_thr(ta, B, st);
     prof_end(pt, st);
     if (e != hipSuccess) return hip_fail(e, "thr_kernel launch");
-    MainArgs ma;
-    ma.X = X; ma.W = W; ma.bias = b; ma.B = B; ma.d = d; ma.F = F;
-    ma.k = (int)k; ma.cap = p.cap;
-    ma.num_tiles = p.num_tiles; ma.tiles_per_wg = p.tpw;
-    ma.thr0 = thr;
-    ma.sampled = p.sample ? 1 : 0;
-    ma.samp_log2 = p.samp_log2;
-    ma.list_keys = list_keys; ma.list_cnt = list_cnt; ma.list_cap = p.list_cap;
-    int pm = prof_begin("main_kernel", st);
-    e = launch_main(dt, p.NB, ma, dim3((unsigned)p.nwg, (unsigned)p.nbc), st);
-    prof_end(pm, st);
-    if (e != hipSuccess) return hip_fail(e, "main_kernel launch");
     MergeArgs mg;
-    mg.list_keys = list_keys; mg.list_cnt = list_cnt; mg.list_cap = p.list_cap;
+    if (p.large) {
+        MainLArgs ml;
+        ml.X = X; ml.W = W; ml.bias = b; ml.B = B; ml.d = d; ml.F = F;
+        ml.k = (int)k; ml.cap = p.cap;
+        ml.num_tiles = p.num_tiles; ml.tiles_per_wg = p.tpw;
+        ml.nbc = (int)p.nbc; ml.nr = p.nwg;
+        ml.thr0 = thr;
+        ml.sampled = p.sample ? 1 : 0;
+        ml.samp_log2 = p.samp_log2;
+        ml.list_keys = list_keys; ml.list_cap = p.list_cap; ml.head_span = p.head_span;
+        ml.seg_cnt = (int32_t*)(ws + p.off_seg);
+        int pm = prof_begin("main_kernel", st);
+        e = launch_mainl(dt, ml, (int)(p.nbc * p.nwg), st);
+        prof_end(pm, st);
+        if (e != hipSuccess) return hip_fail(e, "mainl_kernel launch");
+        mg.list_keys = list_keys; mg.list_cnt = list_cnt; mg.list_cap = p.list_cap;
+        mg.head_span = p.head_span; mg.nseg = p.nwg; mg.seg_cap = p.cap; mg.seg_cnt = ml.seg_cnt;
+    } else {
+        MainArgs ma;
+        ma.X = X; ma.W = W; ma.bias = b; ma.B = B; ma.d = d; ma.F = F;
+        ma.k = (int)k; ma.cap = p.cap;
+        ma.num_tiles = p.num_tiles; ma.tiles_per_wg = p.tpw;
+        ma.thr0 = thr;
+        ma.sampled = p.sample ? 1 : 0;
+        ma.samp_log2 = p.samp_log2;
+        ma.list_keys = list_keys; ma.list_cnt = list_cnt; ma.list_cap = p.list_cap;
+        int pm = prof_begin("main_kernel", st);
+        e = launch_main(dt, p.NB, ma, dim3((unsigned)p.nwg, (unsigned)p.nbc), st);
+        prof_end(pm, st);
+        if (e != hipSuccess) return hip_fail(e, "main_kernel launch");
+        mg.list_keys = list_keys; mg.list_cnt = list_cnt; mg.list_cap = p.list_cap;
+        mg.head_span = p.list_cap; mg.nseg = 0; mg.seg_cap = 1; mg.seg_cnt = nullptr;
+    }
     mg.k = (int)k;
     mg.V = V; mg.I = I;
-    pm = prof_begin("merge_kernel", st);
+    const int pg = prof_begin("merge_kernel", st);
     e = launch_merge(mg, B, st);
-    prof_end(pm, st);
+    prof_end(pg, st);
     if (e != hipSuccess) return hip_fail(e, "merge_kernel launch");
     return 0;
 }

@@ -63,10 +63,39 @@ struct ThrArgs {
     int64_t list_cap;
 };
 
+// Large-batch streaming kernel: 256 rows x 256 latents per tile, queues in
+// global memory (one segment of `cap` keys per row and W range).
+constexpr int kLargeRows = 256;
+constexpr int kLargeThreads = 256;
+constexpr int64_t kLargeMinB = 512;   // batches from this size use mainl_kernel
+
+struct MainLArgs {
+    const void* X;
+    const void* W;
+    const float* bias;
+    int64_t B, d, F;
+    int k, cap;
+    int64_t num_tiles, tiles_per_wg;
+    int nbc, nr;                 // row blocks, W ranges (grid = nbc * nr)
+    const uint64_t* thr0;        // per-row starting threshold keys
+    int sampled, samp_log2;
+    uint64_t* list_keys;         // [B][list_cap]: head_span head slots, then nr segments of cap
+    int64_t list_cap, head_span;
+    int32_t* seg_cnt;            // [B][nr] keys in each segment
+};
+
+// A row's candidates: slots [0, head_span) hold list_cnt[row] keys at their
+// front; then nseg segments of seg_cap slots, segment s holding
+// seg_cnt[row * nseg + s] keys at its front.  With nseg == 0 the row is the
+// dense list [0, list_cnt[row]).
+constexpr int kMergeMaxSeg = 1024;
+
 struct MergeArgs {
     const uint64_t* list_keys;   // [B][list_cap]
     const int32_t* list_cnt;     // [B]
-    int64_t list_cap;
+    int64_t list_cap, head_span;
+    int nseg, seg_cap;
+    const int32_t* seg_cnt;      // [B][nseg]
     int k;
     float* V;
     int32_t* I;
@@ -93,9 +122,11 @@ struct CandArgs {                // approximate variant, top-k over the candidat
 };
 
 size_t main_lds_bytes(int NB, int cap);
+size_t mainl_lds_bytes(int cap);
 size_t group_lds_bytes(int NB);
 
 hipError_t launch_main(int dt, int NB, const MainArgs& a, dim3 grid, hipStream_t st);
+hipError_t launch_mainl(int dt, const MainLArgs& a, int grid, hipStream_t st);
 hipError_t launch_sample(int dt, const SampleArgs& a, dim3 grid, hipStream_t st);
 hipError_t launch_thr(const ThrArgs& a, int64_t rows, hipStream_t st);
 hipError_t launch_merge(const MergeArgs& a, int64_t rows, hipStream_t st);

@@ -313,19 +313,25 @@ __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
     }
 }
 
-// Per row: top-k of the candidate list, read in chunks of kPer keys per
-// thread.  Each chunk is filtered against the larger of its own k-th of the
-// per-thread maxima and the k-th key of the last compaction.
+// Per row: top-k of its candidates (MergeArgs: a dense head, then optional
+// fixed-size segments), read in chunks of kPer slots per thread.  Each chunk
+// is filtered against the larger of its own k-th of the per-thread maxima and
+// the k-th key of the last compaction.
 __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
 {
     constexpr int kPer = 16;
     __shared__ SelShared S;
+    __shared__ int scnt[kMergeMaxSeg];
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
     const int k = a.k;
-    const int64_t n = a.list_cnt[row];
+    const int nseg = a.nseg;
+    const int64_t hc = a.list_cnt[row];
     const uint64_t* keys = a.list_keys + row * a.list_cap;
+    for (int sg = tid; sg < nseg; sg += kThreads) scnt[sg] = a.seg_cnt[row * nseg + sg];
+    const int64_t n = nseg ? a.head_span + (int64_t)nseg * a.seg_cap : hc;
     if (tid == 0) S.cnt = 0;
+    __syncthreads();
     uint64_t run = 0;
     for (int64_t c0 = 0; c0 < n; c0 += (int64_t)kPer * kThreads) {
         uint64_t v[kPer];
@@ -333,7 +339,15 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
 #pragma unroll
         for (int u = 0; u < kPer; ++u) {
             const int64_t i = c0 + tid + (int64_t)u * kThreads;
-            v[u] = i < n ? keys[i] : 0ull;
+            bool ok = i < n;
+            if (ok && i >= a.head_span) {
+                const int jj = (int)(i - a.head_span);
+                const int sg = jj / a.seg_cap;
+                ok = jj - sg * a.seg_cap < scnt[sg];
+            } else if (ok) {
+                ok = i < hc;
+            }
+            v[u] = ok ? keys[i] : 0ull;
         }
 #pragma unroll
         for (int u = 0; u < kPer; ++u) m = v[u] > m ? v[u] : m;

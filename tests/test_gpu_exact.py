@@ -249,3 +249,53 @@ def test_exact_headline_large_bias(cuda_dev):
     b[j] = 1e4
     V, I = _run_check(X, W, b, C2["k"], "bf16", scores="torch64", name="headline/bias")
     assert torch.all(I[:, 0] == j)
+
+
+# Large batches (B >= 512) run the 256-row streaming kernel with per-workgroup
+# queue segments in global memory.
+LARGE = {
+    "large_sampled": dict(B=512, d=256, F=20000, k=128),
+    "large_unsampled_ragged": dict(B=600, d=128, F=3000, k=16),
+    "large_k64": dict(B=1024, d=512, F=40000, k=64),
+}
+
+
+@pytest.mark.parametrize("shape", list(LARGE))
+@pytest.mark.parametrize("dtype_name", ["fp32", "fp16", "bf16"])
+def test_exact_large_batch(cuda_dev, shape, dtype_name):
+    c = LARGE[shape]
+    print(f"case large {shape} {dtype_name} {c}", flush=True)
+    X, W, b = make_inputs(c["B"], c["d"], c["F"], DT[dtype_name], seed=31, device=cuda_dev)
+    _run_check(X, W, b, c["k"], dtype_name, scores="torch64", name=f"{shape}/{dtype_name}")
+
+
+@pytest.mark.parametrize("k", [1, 2, 4, 8, 16, 32, 64, 128])
+def test_exact_large_batch_k_sweep(cuda_dev, k):
+    print(f"case large k-sweep k={k}", flush=True)
+    X, W, b = make_inputs(513, 128, 16384 + 300, torch.bfloat16, seed=32, device=cuda_dev)
+    _run_check(X, W, b, k, "bf16", scores="torch64", name=f"large k={k}")
+
+
+@pytest.mark.parametrize("F", [8000, 20480])
+def test_large_batch_increasing_scores_adversarial(cuda_dev, F):
+    """Scores increase along F: every segment overflows and is compacted on
+    every tile, in the large-batch kernel."""
+    print(f"case large increasing F={F}", flush=True)
+    B, d, k = 512, 64, 128
+    X = torch.ones(B, d, dtype=torch.float32, device=cuda_dev)
+    W = torch.zeros(F, d, dtype=torch.float32, device=cuda_dev)
+    b = torch.arange(F, dtype=torch.float32, device=cuda_dev) * 1e-3
+    V, I = topk_sae_cuda_exact(X, W, b, k)
+    want = np.arange(F - 1, F - 1 - k, -1)
+    In = I.cpu().numpy()
+    assert all(np.array_equal(In[i], want) for i in range(B))
+    assert np.array_equal(V[0].cpu().numpy(), b.cpu().numpy()[want])
+
+
+@pytest.mark.parametrize("heavy", [False, True])
+def test_exact_config4_shape(cuda_dev, heavy):
+    """BASELINE config 4 at full size (B=1024 d=4096 F=262144 k=128), with and
+    without the heavy-tailed W_enc (1% of rows scaled 5x)."""
+    print(f"case config4 heavy={heavy}", flush=True)
+    X, W, b = make_inputs(1024, 4096, 262144, torch.bfloat16, seed=0, device=cuda_dev, heavy_tail=heavy)
+    _run_check(X, W, b, 128, "bf16", scores="torch64", name=f"config4/heavy={heavy}")
