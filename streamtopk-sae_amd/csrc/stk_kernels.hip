@@ -118,6 +118,9 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
                 if (m == 0) continue;
                 const int j = 32 * n + jl;
                 const int base = atomicAdd(&cnt[j], __builtin_popcount(m));
+                // resolve `base` once: otherwise every per-bit store below waits
+                // lgkmcnt(0), and with it for the previous bit's store
+                __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
                 uint64_t* qj = q + (size_t)j * cap;
                 uint32_t keep = 0;
 #pragma unroll
