@@ -112,21 +112,23 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
         // ---- append; compact full queues and retry while anything overflowed ----
         for (int it = 0; it < 4096; ++it) {
             bool overflow = false;
+            // reserve the slots of every row block first, then wait once
+            int base[NB];
+#pragma unroll
+            for (int n = 0; n < NB; ++n)
+                base[n] = pend[n] ? atomicAdd(&cnt[32 * n + jl], __builtin_popcount(pend[n])) : 0;
+            __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): every per-bit store below may use them
 #pragma unroll
             for (int n = 0; n < NB; ++n) {
                 const uint32_t m = pend[n];
                 if (m == 0) continue;
                 const int j = 32 * n + jl;
-                const int base = atomicAdd(&cnt[j], __builtin_popcount(m));
-                // resolve `base` once: otherwise every per-bit store below waits
-                // lgkmcnt(0), and with it for the previous bit's store
-                __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
                 uint64_t* qj = q + (size_t)j * cap;
                 uint32_t keep = 0;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     if (m >> r & 1u) {
-                        const int slot = base + __builtin_popcount(m & ((1u << r) - 1u));
+                        const int slot = base[n] + __builtin_popcount(m & ((1u << r) - 1u));
                         if (slot < cap)
                             qj[slot] = make_key(ac[0][n][r], fl + (r >> 2) * 8 + (r & 3));
                         else

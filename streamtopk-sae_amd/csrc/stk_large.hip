@@ -7,9 +7,11 @@
 // byte fetched feeds 256 rows and every staged X byte feeds 256 latents.
 //   - W: straight from global memory into registers, 2 d-steps ahead; each
 //     16-byte quad is reloaded as soon as its last MFMA of the step issued.
+//     The pipeline restarts at every tile, so the epilogue holds no prefetch.
 //   - X: 256 rows x 128 bytes per d-step, 2 d-steps ahead in registers, then
 //     through a 2-buffer LDS ring (one barrier per d-step).
-//   - bias: the tile's 256 values are staged in LDS during the tile.
+//   - bias: the tile's 256 values are loaded at the tile start and staged in
+//     LDS for the epilogue.
 //   - epilogue: scores not below the row threshold are appended to the row's
 //     queue segment in global memory (counters in LDS).  A full segment is
 //     rank-compacted to its top-k, which raises the row threshold.
@@ -48,7 +50,7 @@ struct BigStream {
     int ntiles, nds, nds2;
     int tid, lane, wave, h, jl;
 
-    // W and X cursors (2 steps ahead), uniform
+    // W and X cursors (tile, step), uniform; a tile's pipeline ends at the tile
     int wt, ws, xt, xsn;
     __amdgpu_buffer_rsrc_t wres, xres, zres;
     int wvoff[kLFrags];          // row of this lane's latent within the tile, + lane half
@@ -64,7 +66,13 @@ struct BigStream {
         const int64_t nrows = (B - b0 < kLargeRows) ? B - b0 : kLargeRows;
         xres = make_rsrc(X + b0 * row_bytes, nrows * row_bytes);
         zres = make_rsrc(X, 0);
-        set_w_tile(0);
+    }
+
+    __device__ __forceinline__ void begin_tile(int t)
+    {
+        wt = xt = t;
+        ws = xsn = 0;
+        set_w_tile(t);
     }
 
     __device__ __forceinline__ void set_w_tile(int t)
@@ -81,11 +89,7 @@ struct BigStream {
         const bool live = wt < ntiles && ws < nds;
         r = live ? wres : zres;
         so = live ? ws * kStepBytes : 0;
-        if (wt < ntiles && ++ws == nds2) {
-            ws = 0;
-            ++wt;
-            if (wt < ntiles) set_w_tile(wt);
-        }
+        ++ws;
     }
 
     __device__ __forceinline__ void load_wq(u32x4 (&w)[kLFrags][4], int q, __amdgpu_buffer_rsrc_t r, int so) const
@@ -110,10 +114,7 @@ struct BigStream {
         const int so = live ? xsn * kStepBytes : 0;
 #pragma unroll
         for (int p = 0; p < kLXChunks; ++p) x[p] = __builtin_amdgcn_raw_buffer_load_b128(r, xvoff[p], so, 0);
-        if (xt < ntiles && ++xsn == nds2) {
-            xsn = 0;
-            ++xt;
-        }
+        ++xsn;
     }
 
     __device__ __forceinline__ void store_x(const u32x4 (&x)[kLXChunks], unsigned char* xs) const
@@ -158,6 +159,16 @@ struct BigStream {
         __builtin_amdgcn_sched_barrier(0);
     }
 };
+
+// An accumulator element read into a VGPR at the point of use.  Volatile, so
+// the compiler cannot keep VGPR copies of all 256 accumulators alive across
+// the epilogue's passes (which spills).
+__device__ __forceinline__ float agpr_read(float x)
+{
+    float r;
+    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(r) : "a"(x));
+    return r;
+}
 
 // Compacts the segments of this wave's rows that are full to their top-k.
 // Segment keys are read through L2 (agent-scope atomic loads): other waves'
@@ -270,25 +281,9 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
     bs.jl = jl;
 
     if (bs.ntiles > 0) {
-        bs.wt = 0;
-        bs.ws = 0;
-        bs.xt = 0;
-        bs.xsn = 0;
         bs.init();
         u32x4 wA[kLFrags][4], wB[kLFrags][4];
         u32x4 xA[kLXChunks], xB[kLXChunks];
-        // bias of the first tile (the bias of tile t + 1 is loaded in tile t's epilogue)
-        float bnext;
-        {
-            const int64_t f = bs.tile_begin * kLTile + tid;
-            bnext = a.bias[f < F ? f : F - 1];
-        }
-        bs.issue_w(wA);
-        bs.issue_w(wB);
-        bs.issue_x(xA);
-        bs.issue_x(xB);
-        bs.store_x(xA, xs0);
-        bs.issue_x(xA);
 
         f32x16 acc[kLFrags][kLNB];
 #pragma unroll
@@ -300,6 +295,21 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
 
         for (int t = 0; t < bs.ntiles; ++t) {
             const int64_t tile0 = (bs.tile_begin + t) * kLTile;
+            // The pipeline is restarted per tile so that no prefetch registers are
+            // live in the epilogue (one exposed load latency per tile of nds steps).
+            float bnext;
+            {
+                const int64_t f = tile0 + tid;
+                bnext = a.bias[f < F ? f : F - 1];
+            }
+            bs.begin_tile(t);
+            bs.issue_w(wA);
+            bs.issue_w(wB);
+            bs.issue_x(xA);
+            bs.issue_x(xB);
+            bs.store_x(xA, xs0);
+            bs.issue_x(xA);
+            __syncthreads();
             // a padded last step (s >= nds) reads zeros: every step computes unconditionally
             for (int s = 0; s < bs.nds2; s += 2) {
                 bs.step(acc, wA, xs0);
@@ -313,10 +323,6 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
             }
             bias_s[tid] = bnext;
             __syncthreads();
-            {
-                const int64_t f = tile0 + kLTile + tid;
-                bnext = a.bias[f < F ? f : F - 1];
-            }
 
             // ---- epilogue: bias, threshold filter, append to the row segments ----
             uint32_t vmask[kLFrags];
@@ -340,11 +346,16 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                     vmask[fa] = m;
                 }
             }
-            // Scores are recomputed from the accumulators (AGPRs) and the LDS bias
-            // wherever they are needed, so the epilogue holds no score array.
+            // Scores are read from the accumulators (AGPRs) at each use and the
+            // bias of this lane's 32 latents is held in VGPRs; the prefetch
+            // registers are dead here.
             // Latent of bit 16*fa + r of a row mask: lat0 + fa*32 + 8*(r/4) + r%4.
             const int lat0 = (int)tile0 + wave * 64 + h * 4;
-            const float* bw = bias_s + wave * 64 + h * 4;
+            float bl[kLFrags * 16];
+#pragma unroll
+            for (int fa = 0; fa < kLFrags; ++fa)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) bl[fa * 16 + r] = bias_s[wave * 64 + h * 4 + fa * 32 + (r >> 2) * 8 + (r & 3)];
             uint32_t pend[kLNB];
 #pragma unroll
             for (int n = 0; n < kLNB; ++n) {
@@ -355,40 +366,47 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
 #pragma unroll
                 for (int fa = 0; fa < kLFrags; ++fa)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const float sc = acc[fa][n][r] + bw[fa * 32 + (r >> 2) * 8 + (r & 3)];
-                        m |= (!(sc < tv)) ? (1u << (16 * fa + r)) : 0u;
-                    }
+                    for (int r = 0; r < 16; ++r)
+                        m |= (!(agpr_read(acc[fa][n][r]) + bl[fa * 16 + r] < tv)) ? (1u << (16 * fa + r)) : 0u;
                 m &= vmask[0] | (vmask[1] << 16);
                 pend[n] = (b0 + j < B) ? m : 0u;
             }
             for (int it = 0; it < 1 << 20; ++it) {
                 bool overflow = false;
+                // reserve the slots of every row block first, then wait once
+                int base[kLNB];
+#pragma unroll
+                for (int n = 0; n < kLNB; ++n)
+                    base[n] = pend[n] ? atomicAdd(&cnt[32 * n + jl], __builtin_popcount(pend[n])) : 0;
+                __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+                // Per row block: the 32 biased scores of every lane go to this
+                // wave's LDS staging area (the X buffers are idle here), then each
+                // lane walks only its own set bits and reads each score back by
+                // address: max-popcount iterations instead of 32 divergent blocks.
+                float* stage = (float*)xs0 + wave * (kLFrags * 16 * 64);
 #pragma unroll
                 for (int n = 0; n < kLNB; ++n) {
                     const uint32_t m = pend[n];
-                    if (m == 0) continue;
-                    const int j = 32 * n + jl;
-                    const int base = atomicAdd(&cnt[j], __builtin_popcount(m));
-                    // resolve `base` once: otherwise every per-bit store below waits
-                    // lgkmcnt(0), and with it for the previous bit's store
-                    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
-                    uint64_t* q = qrow[j];
-                    uint32_t keep = 0;
+                    if (__ballot(m != 0) == 0) continue;
 #pragma unroll
                     for (int fa = 0; fa < kLFrags; ++fa)
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int bit = 16 * fa + r;
-                            if (m >> bit & 1u) {
-                                const int slot = base + __builtin_popcount(m & ((1u << bit) - 1u));
-                                const int off = fa * 32 + (r >> 2) * 8 + (r & 3);
-                                if (slot < cap)
-                                    q[slot] = make_key(acc[fa][n][r] + bw[off], lat0 + off);
-                                else
-                                    keep |= 1u << bit;
-                            }
+                        for (int r = 0; r < 16; ++r)
+                            stage[(fa * 16 + r) * 64 + lane] = agpr_read(acc[fa][n][r]) + bl[fa * 16 + r];
+                    uint64_t* q = qrow[32 * n + jl];
+                    uint32_t keep = 0, mm = m;
+                    int slot = base[n];
+                    while (mm) {
+                        const int bit = __builtin_ctz(mm);
+                        mm &= mm - 1u;
+                        if (slot < cap) {
+                            const int off = (bit >> 4) * 32 + ((bit & 15) >> 2) * 8 + (bit & 3);
+                            q[slot] = make_key(stage[bit * 64 + lane], lat0 + off);
+                        } else {
+                            keep |= 1u << bit;
                         }
+                        ++slot;
+                    }
                     pend[n] = keep;
                     overflow |= keep != 0;
                 }
@@ -408,7 +426,8 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                         for (int r = 0; r < 16; ++r) {
                             const int bit = 16 * fa + r;
                             const int off = fa * 32 + (r >> 2) * 8 + (r & 3);
-                            if ((pend[n] >> bit & 1u) && !(make_key(acc[fa][n][r] + bw[off], lat0 + off) > tk))
+                            if ((pend[n] >> bit & 1u) &&
+                                !(make_key(agpr_read(acc[fa][n][r]) + bl[fa * 16 + r], lat0 + off) > tk))
                                 pend[n] &= ~(1u << bit);
                         }
                 }
@@ -420,9 +439,8 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) acc[fa][n][r] = 0.f;
             // The epilogue issued a data-dependent number of queue stores, which
-            // the compiler cannot count; waiting for them here (the next tile's
-            // first loads completed long ago) lets it keep exact vmcnt waits in
-            // the d-step loop instead of vmcnt(0).
+            // the compiler cannot count; waiting for them here lets it keep
+            // exact vmcnt waits in the next tile's d-step loop.
             __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
         }
     }
