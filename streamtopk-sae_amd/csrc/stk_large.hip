@@ -127,6 +127,11 @@ struct BigStream {
     // One d-step.  The X operands of all 8 row blocks for quad q + 1 are read
     // from LDS while the 16 MFMAs of quad q run; after them, quad q of this
     // wave's W is reloaded with the step two ahead (its last use has issued).
+    // One d-step on LDS buffer `xs`.  Each quad interleaves its 16 MFMAs with
+    // the 8 LDS reads of the next quad and the reloads of its own W registers,
+    // so those issue while an MFMA executes: the MFMAs of fragment 0 come
+    // first (reads interleaved), then fragment 1, with fragment 0's W reload
+    // issued among them.
     __device__ __forceinline__ void step(f32x16 (&acc)[kLFrags][kLNB], u32x4 (&w)[kLFrags][4],
                                          const unsigned char* xs)
     {
@@ -137,26 +142,33 @@ struct BigStream {
         u32x4 bA[kLNB], bB[kLNB];
 #pragma unroll
         for (int n = 0; n < kLNB; ++n) bA[n] = *(const u32x4*)(xl + (32 * n) * kXRowStride);
-        // (scheduling barriers keep the compiler from sinking the reads to
-        // their uses, which would expose the LDS latency on every MFMA pair)
+        __builtin_amdgcn_sched_barrier(0);   // quad 0's operands are all in flight before any MFMA
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             u32x4 (&cur)[kLNB] = (q & 1) ? bB : bA;
             u32x4 (&nxt)[kLNB] = (q & 1) ? bA : bB;
-            __builtin_amdgcn_sched_barrier(0);
             if (q < 3) {
 #pragma unroll
                 for (int n = 0; n < kLNB; ++n) nxt[n] = *(const u32x4*)(xl + (32 * n) * kXRowStride + (q + 1) * 16);
             }
-            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int n = 0; n < kLNB; ++n)
+            for (int n = 0; n < kLNB; ++n) mfma_quad<DT>(acc[0][n], w[0][q], cur[n]);
+            w[0][q] = __builtin_amdgcn_raw_buffer_load_b128(r, wvoff[0] + q * 16, so, 0);
 #pragma unroll
-                for (int a = 0; a < kLFrags; ++a) mfma_quad<DT>(acc[a][n], w[a][q], cur[n]);
+            for (int n = 0; n < kLNB; ++n) mfma_quad<DT>(acc[1][n], w[1][q], cur[n]);
+            w[1][q] = __builtin_amdgcn_raw_buffer_load_b128(r, wvoff[1] + q * 16, so, 0);
+            // pattern: (MFMA, DS read) x 8, (MFMA, VMEM read), MFMA x 7, then the last VMEM
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                if (q < 3) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM read
+            __builtin_amdgcn_sched_group_barrier(0x008, 7, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
             __builtin_amdgcn_sched_barrier(0);
-            load_wq(w, q, r, so);
         }
-        __builtin_amdgcn_sched_barrier(0);
     }
 };
 
