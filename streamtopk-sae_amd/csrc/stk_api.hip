@@ -115,6 +115,7 @@ struct ExactPlan {
     int nwg;                     // main_kernel: W ranges; mainl_kernel: nr (grid = nbc * nr)
     bool sample;
     int samp_log2;
+    int ksplit;                  // large batches: d ranges of the sample pass
     int64_t list_cap, head_span;
     size_t off_thr, off_P, off_list, off_lcnt, off_seg, total;
 };
@@ -122,8 +123,6 @@ struct ExactPlan {
 static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int dtype, int ncu)
 {
     ExactPlan p;
-    (void)d;
-    (void)dtype;
     p.num_tiles = cdiv(F, kTileLatents);
     p.large = B >= kLargeMinB;
     if (p.large) {
@@ -158,13 +157,25 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
         // kSampleBlocks blocks of kSampleBlock consecutive latents, 1 << samp_log2 apart
         p.samp_log2 = ilog2_floor(F / kSampleBlocks);
     }
+    // large batches score the sample with mainl_kernel's sample mode: one
+    // workgroup per (row block, 256 sampled latents, d range), enough d
+    // ranges to fill the device
+    p.ksplit = 1;
+    if (p.large && p.sample) {
+        const int64_t wgs = p.nbc * (kSampleTarget / kTileLatents);
+        int64_t ks = cdiv(ncu, wgs);
+        const int64_t nds = d / (dtype == STK_DTYPE_F32 ? 32 : 64);
+        if (ks > nds) ks = nds;
+        if (ks < 1) ks = 1;
+        p.ksplit = (int)ks;
+    }
     p.head_span = p.sample ? kSampleTarget : 0;
     p.list_cap = p.head_span + (int64_t)p.nwg * p.cap;
     size_t off = 0;
     p.off_thr = off;
     off = align256(off + (size_t)B * 8);
     p.off_P = off;
-    if (p.sample) off = align256(off + (size_t)B * kSampleTarget * 4);
+    if (p.sample) off = align256(off + (size_t)p.ksplit * B * kSampleTarget * 4);
     p.off_list = off;
     off = align256(off + (size_t)B * p.list_cap * 8);
     p.off_lcnt = off;
@@ -227,7 +238,21 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     uint64_t* list_keys = (uint64_t*)(ws + p.off_list);
     int32_t* list_cnt = (int32_t*)(ws + p.off_lcnt);
     float* P = p.sample ? (float*)(ws + p.off_P) : nullptr;
-    if (p.sample) {
+    if (p.sample && p.large) {
+        MainLArgs sl;
+        std::memset(&sl, 0, sizeof sl);
+        sl.X = X; sl.W = W; sl.bias = b; sl.B = B; sl.d = d; sl.F = F;
+        sl.k = (int)k; sl.cap = p.cap;
+        sl.nbc = (int)p.nbc;
+        sl.samp_log2 = p.samp_log2;
+        sl.ksplit = p.ksplit;
+        sl.P = P;
+        const int grid = (int)(p.nbc * (kSampleTarget / kTileLatents) * p.ksplit);
+        int pi = prof_begin("sample_kernel", st);
+        e = launch_mainl_sample(dt, sl, grid, st);
+        prof_end(pi, st);
+        if (e != hipSuccess) return hip_fail(e, "sample launch");
+    } else if (p.sample) {
         SampleArgs sa;
         sa.X = X; sa.W = W; sa.bias = b; sa.B = B; sa.d = d;
         sa.samp_log2 = p.samp_log2;
@@ -239,6 +264,8 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     }
     ThrArgs ta;
     ta.P = P;
+    ta.nsplit = p.large ? p.ksplit : 1;
+    ta.bias = p.large ? b : nullptr;   // sample_kernel adds the bias itself
     ta.samp_log2 = p.samp_log2; ta.k = (int)k;
     ta.thr = thr; ta.list_keys = list_keys; ta.list_cnt = list_cnt; ta.list_cap = p.list_cap;
     int pt = prof_begin("thr_kernel", st);
@@ -248,6 +275,7 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     MergeArgs mg;
     if (p.large) {
         MainLArgs ml;
+        std::memset(&ml, 0, sizeof ml);
         ml.X = X; ml.W = W; ml.bias = b; ml.B = B; ml.d = d; ml.F = F;
         ml.k = (int)k; ml.cap = p.cap;
         ml.num_tiles = p.num_tiles; ml.tiles_per_wg = p.tpw;

@@ -55,7 +55,10 @@ struct SampleArgs {
 };
 
 struct ThrArgs {
-    const float* P;              // sampled scores, or null (no sample: threshold 0)
+    const float* P;              // sampled scores, or null (no sample: threshold 0):
+                                 //   nsplit partial sums [nsplit][B][kSampleTarget]
+    int nsplit;                  //   added in split order, then
+    const float* bias;           //   + bias[latent] if non-null
     int samp_log2, k;
     uint64_t* thr;               // [B] row threshold keys
     uint64_t* list_keys;         // [B][list_cap]: receives the sampled keys >= thr
@@ -82,6 +85,10 @@ struct MainLArgs {
     uint64_t* list_keys;         // [B][list_cap]: head_span head slots, then nr segments of cap
     int64_t list_cap, head_span;
     int32_t* seg_cnt;            // [B][nr] keys in each segment
+    // sample mode (mainl_sample_kernel): 256-latent tiles of the sampled
+    // latents, d split in ksplit ranges; raw partial scores to P
+    int ksplit;
+    float* P;                    // [ksplit][B][kSampleTarget]
 };
 
 // A row's candidates: slots [0, head_span) hold list_cnt[row] keys at their
@@ -127,6 +134,7 @@ size_t group_lds_bytes(int NB);
 
 hipError_t launch_main(int dt, int NB, const MainArgs& a, dim3 grid, hipStream_t st);
 hipError_t launch_mainl(int dt, const MainLArgs& a, int grid, hipStream_t st);
+hipError_t launch_mainl_sample(int dt, const MainLArgs& a, int grid, hipStream_t st);
 hipError_t launch_sample(int dt, const SampleArgs& a, dim3 grid, hipStream_t st);
 hipError_t launch_thr(const ThrArgs& a, int64_t rows, hipStream_t st);
 hipError_t launch_merge(const MergeArgs& a, int64_t rows, hipStream_t st);

@@ -291,9 +291,18 @@ __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
         return;
     }
     const float* prow = a.P + row * kSampleTarget;
+    const int64_t split_stride = (int64_t)gridDim.x * kSampleTarget;   // B rows per split
     float v[kItems];
 #pragma unroll
     for (int t = 0; t < kItems; ++t) v[t] = prow[tid + t * kThreads];
+    for (int sp = 1; sp < a.nsplit; ++sp) {
+#pragma unroll
+        for (int t = 0; t < kItems; ++t) v[t] += prow[sp * split_stride + tid + t * kThreads];
+    }
+    if (a.bias != nullptr) {
+#pragma unroll
+        for (int t = 0; t < kItems; ++t) v[t] += a.bias[sample_latent(tid + t * kThreads, a.samp_log2)];
+    }
     uint64_t key[kItems];
     uint64_t m = 0;
 #pragma unroll

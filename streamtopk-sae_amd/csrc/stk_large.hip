@@ -18,6 +18,10 @@
 //   - grid: workgroups are placed so that the row blocks sharing a W range
 //     run on one XCD (workgroup i runs on XCD i % 8), and W is fetched into
 //     that XCD's L2 once for all of them.
+// mainl_kernel<DT, true> (sample mode) computes the raw scores of the
+// sampled latents with the same machinery: one 256-latent tile of them per
+// workgroup and a d range per workgroup, partial sums summed in a fixed order
+// by thr_kernel.
 // The reference has no counterpart: its B >= #SMs path streams all of W per
 // row (streamtopk_exact.cu:506-638).
 #include "stk_kernels.h"
@@ -40,7 +44,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_records, 0x00020000);
 }
 
-template <int DT>
+template <int DT, bool SAMPLE>
 struct BigStream {
     const unsigned char* W;
     int64_t row_bytes;           // bytes of a W row and of an X row (d elements)
@@ -48,6 +52,8 @@ struct BigStream {
     int64_t B, b0, F;
     int64_t tile_begin;
     int ntiles, nds, nds2;
+    int s_lo, s_hi;              // d-steps [s_lo, s_hi) of every tile
+    int samp_log2;               // SAMPLE: tile t covers sampled latents t*256 ..
     int tid, lane, wave, h, jl;
 
     // W and X cursors (tile, step), uniform; a tile's pipeline ends at the tile
@@ -58,9 +64,12 @@ struct BigStream {
 
     __device__ __forceinline__ void init()
     {
+        // encode: offsets within the tile; sample: within this wave's 64-latent
+        // run of a sampled block (its own resource base)
+        const int wbase = SAMPLE ? 0 : wave * (32 * kLFrags);
 #pragma unroll
         for (int a = 0; a < kLFrags; ++a)
-            wvoff[a] = (wave * (32 * kLFrags) + a * 32 + jl) * (int)row_bytes + h * 64;
+            wvoff[a] = (wbase + a * 32 + jl) * (int)row_bytes + h * 64;
 #pragma unroll
         for (int p = 0; p < kLXChunks; ++p) xvoff[p] = ((tid >> 3) + 32 * p) * (int)row_bytes + (tid & 7) * 16;
         const int64_t nrows = (B - b0 < kLargeRows) ? B - b0 : kLargeRows;
@@ -71,22 +80,28 @@ struct BigStream {
     __device__ __forceinline__ void begin_tile(int t)
     {
         wt = xt = t;
-        ws = xsn = 0;
+        ws = xsn = s_lo;
         set_w_tile(t);
     }
 
     __device__ __forceinline__ void set_w_tile(int t)
     {
         const int64_t tile0 = (tile_begin + t) * kLTile;
-        int64_t n = F - tile0;
-        n = n < kLTile ? (n > 0 ? n : 0) : kLTile;
-        wres = make_rsrc(W + tile0 * row_bytes, n * row_bytes);
+        if (SAMPLE) {
+            // the wave's 64 sampled latents are consecutive latents of one block
+            const int64_t f0 = sample_latent(tile0 + wave * (32 * kLFrags), samp_log2);
+            wres = make_rsrc(W + f0 * row_bytes, (int64_t)(32 * kLFrags) * row_bytes);
+        } else {
+            int64_t n = F - tile0;
+            n = n < kLTile ? (n > 0 ? n : 0) : kLTile;
+            wres = make_rsrc(W + tile0 * row_bytes, n * row_bytes);
+        }
     }
 
     // Resource and step offset of the W cursor's step; advances the cursor.
     __device__ __forceinline__ void next_w(__amdgpu_buffer_rsrc_t& r, int& so)
     {
-        const bool live = wt < ntiles && ws < nds;
+        const bool live = wt < ntiles && ws < s_hi;
         r = live ? wres : zres;
         so = live ? ws * kStepBytes : 0;
         ++ws;
@@ -109,7 +124,7 @@ struct BigStream {
 
     __device__ __forceinline__ void issue_x(u32x4 (&x)[kLXChunks])
     {
-        const bool live = xt < ntiles && xsn < nds;
+        const bool live = xt < ntiles && xsn < s_hi;
         const __amdgpu_buffer_rsrc_t r = live ? xres : zres;
         const int so = live ? xsn * kStepBytes : 0;
 #pragma unroll
@@ -232,7 +247,7 @@ size_t mainl_lds_bytes(int cap)
            (size_t)kLWaves * cap * 8 + (size_t)kLargeRows * sizeof(uint64_t*);
 }
 
-template <int DT>
+template <int DT, bool SAMPLE>
 __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
 {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -248,11 +263,17 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, jl = lane & 31;
 
-    // workgroup -> (row block, W range): the row blocks of a W range share an XCD
-    int rb, rg;
+    // workgroup -> (row block, W range): the row blocks of a W range share an XCD.
+    // Sample mode: workgroup -> (row block, sample tile, d range).
+    constexpr int kSampleTiles = kSampleTarget / kLTile;
+    int rb, rg, ks = 0;
     {
         const int id = blockIdx.x;
-        if ((a.nr & 7) == 0) {
+        if (SAMPLE) {
+            rb = id % a.nbc;
+            rg = (id / a.nbc) % kSampleTiles;
+            ks = id / (a.nbc * kSampleTiles);
+        } else if ((a.nr & 7) == 0) {
             const int slot = id >> 3;
             rb = slot % a.nbc;
             rg = (slot / a.nbc) * 8 + (id & 7);
@@ -264,28 +285,38 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
     const int64_t b0 = (int64_t)rb * kLargeRows;
     const int64_t B = a.B, F = a.F;
 
-    for (int i = tid; i < kLargeRows; i += kLargeThreads) {
-        const int64_t row = b0 + i;
-        cnt[i] = 0;
-        thr[i] = (row < B) ? a.thr0[row] : 0ull;
-        qrow[i] = a.list_keys + ((row < B) ? row : 0) * a.list_cap + a.head_span + (int64_t)rg * cap;
+    if (!SAMPLE) {
+        for (int i = tid; i < kLargeRows; i += kLargeThreads) {
+            const int64_t row = b0 + i;
+            cnt[i] = 0;
+            thr[i] = (row < B) ? a.thr0[row] : 0ull;
+            qrow[i] = a.list_keys + ((row < B) ? row : 0) * a.list_cap + a.head_span + (int64_t)rg * cap;
+        }
     }
 
-    BigStream<DT> bs;
+    BigStream<DT, SAMPLE> bs;
     bs.W = (const unsigned char*)a.W;
     bs.row_bytes = a.d * Dt<DT>::esize;
     bs.X = (const unsigned char*)a.X;
     bs.B = B;
     bs.b0 = b0;
     bs.F = F;
-    bs.tile_begin = (int64_t)rg * a.tiles_per_wg;
-    {
+    bs.nds = (int)(a.d / Dt<DT>::DS);
+    bs.samp_log2 = a.samp_log2;
+    if (SAMPLE) {
+        bs.tile_begin = rg;
+        bs.ntiles = 1;
+        bs.s_lo = (int)((int64_t)ks * bs.nds / a.ksplit);
+        bs.s_hi = (int)((int64_t)(ks + 1) * bs.nds / a.ksplit);
+    } else {
+        bs.tile_begin = (int64_t)rg * a.tiles_per_wg;
         const int64_t t1 = bs.tile_begin + a.tiles_per_wg;
         const int64_t nt = (t1 < a.num_tiles ? t1 : a.num_tiles) - bs.tile_begin;
         bs.ntiles = nt > 0 ? (int)nt : 0;
+        bs.s_lo = 0;
+        bs.s_hi = bs.nds;
     }
-    bs.nds = (int)(a.d / Dt<DT>::DS);
-    bs.nds2 = (bs.nds + 1) / 2 * 2;
+    bs.nds2 = (bs.s_hi - bs.s_lo + 1) / 2 * 2;
     bs.tid = tid;
     bs.lane = lane;
     bs.wave = wave;
@@ -309,8 +340,8 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
             const int64_t tile0 = (bs.tile_begin + t) * kLTile;
             // The pipeline is restarted per tile so that no prefetch registers are
             // live in the epilogue (one exposed load latency per tile of nds steps).
-            float bnext;
-            {
+            float bnext = 0.f;
+            if (!SAMPLE) {
                 const int64_t f = tile0 + tid;
                 bnext = a.bias[f < F ? f : F - 1];
             }
@@ -332,6 +363,27 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                 bs.store_x(xA, xs0);
                 bs.issue_x(xA);
                 __syncthreads();
+            }
+            if (SAMPLE) {
+                // raw partial scores of this d range: P[ks][row][sample index]
+                float* P = a.P + (int64_t)ks * B * kSampleTarget;
+#pragma unroll
+                for (int n = 0; n < kLNB; ++n) {
+                    const int64_t row = b0 + 32 * n + jl;
+                    if (row < B) {
+#pragma unroll
+                        for (int fa = 0; fa < kLFrags; ++fa)
+#pragma unroll
+                            for (int r4 = 0; r4 < 4; ++r4) {
+                                const int64_t i = tile0 + wave * 64 + fa * 32 + r4 * 8 + h * 4;
+                                f32x4 v;
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) v[e] = acc[fa][n][r4 * 4 + e];
+                                *(f32x4*)(P + row * kSampleTarget + i) = v;
+                            }
+                    }
+                }
+                continue;
             }
             bias_s[tid] = bnext;
             __syncthreads();
@@ -457,6 +509,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
         }
     }
 
+    if (SAMPLE) return;
     __syncthreads();
     for (int i = tid; i < kLargeRows; i += kLargeThreads) {
         const int64_t row = b0 + i;
@@ -464,11 +517,11 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
     }
 }
 
-template <int DT>
+template <int DT, bool SAMPLE>
 static hipError_t launch_mainl_t(const MainLArgs& a, int grid, hipStream_t st)
 {
     const size_t lds = mainl_lds_bytes(a.cap);
-    auto kern = mainl_kernel<DT>;
+    auto kern = mainl_kernel<DT, SAMPLE>;
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kLargeThreads), lds, st, a);
@@ -477,9 +530,17 @@ static hipError_t launch_mainl_t(const MainLArgs& a, int grid, hipStream_t st)
 
 hipError_t launch_mainl(int dt, const MainLArgs& a, int grid, hipStream_t st)
 {
-    if (dt == DT_BF16) return launch_mainl_t<DT_BF16>(a, grid, st);
-    if (dt == DT_F16) return launch_mainl_t<DT_F16>(a, grid, st);
-    if (dt == DT_F32) return launch_mainl_t<DT_F32>(a, grid, st);
+    if (dt == DT_BF16) return launch_mainl_t<DT_BF16, false>(a, grid, st);
+    if (dt == DT_F16) return launch_mainl_t<DT_F16, false>(a, grid, st);
+    if (dt == DT_F32) return launch_mainl_t<DT_F32, false>(a, grid, st);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_mainl_sample(int dt, const MainLArgs& a, int grid, hipStream_t st)
+{
+    if (dt == DT_BF16) return launch_mainl_t<DT_BF16, true>(a, grid, st);
+    if (dt == DT_F16) return launch_mainl_t<DT_F16, true>(a, grid, st);
+    if (dt == DT_F32) return launch_mainl_t<DT_F32, true>(a, grid, st);
     return hipErrorInvalidValue;
 }
 
