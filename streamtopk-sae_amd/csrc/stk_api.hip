@@ -114,7 +114,7 @@ struct ExactPlan {
     int64_t nbc, num_tiles, tpw;
     int nwg;                     // main_kernel: W ranges; mainl_kernel: nr (grid = nbc * nr)
     bool sample;
-    int samp_log2;
+    int samp_log2, nsamp;        // sampled latents: nsamp / kSampleBlock blocks, 1 << samp_log2 apart
     int ksplit;                  // large batches: d ranges of the sample pass
     int64_t list_cap, head_span;
     size_t off_thr, off_P, off_list, off_lcnt, off_seg, total;
@@ -153,29 +153,32 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
 
     p.sample = F >= kSampleMinF;
     p.samp_log2 = 0;
+    p.nsamp = 0;
     if (p.sample) {
-        // kSampleBlocks blocks of kSampleBlock consecutive latents, 1 << samp_log2 apart
-        p.samp_log2 = ilog2_floor(F / kSampleBlocks);
+        // large batches take a twice larger sample: a tighter threshold halves
+        // the candidates their (compute-bound) epilogue and merge handle
+        p.nsamp = (p.large && F >= kSampleLargeMinF) ? kSampleLarge : kSampleTarget;
+        p.samp_log2 = ilog2_floor(F / (p.nsamp / kSampleBlock));
     }
     // large batches score the sample with mainl_kernel's sample mode: one
     // workgroup per (row block, 256 sampled latents, d range), enough d
     // ranges to fill the device
     p.ksplit = 1;
     if (p.large && p.sample) {
-        const int64_t wgs = p.nbc * (kSampleTarget / kTileLatents);
+        const int64_t wgs = p.nbc * (p.nsamp / kTileLatents);
         int64_t ks = cdiv(ncu, wgs);
         const int64_t nds = d / (dtype == STK_DTYPE_F32 ? 32 : 64);
         if (ks > nds) ks = nds;
         if (ks < 1) ks = 1;
         p.ksplit = (int)ks;
     }
-    p.head_span = p.sample ? kSampleTarget : 0;
+    p.head_span = p.sample ? p.nsamp : 0;
     p.list_cap = p.head_span + (int64_t)p.nwg * p.cap;
     size_t off = 0;
     p.off_thr = off;
     off = align256(off + (size_t)B * 8);
     p.off_P = off;
-    if (p.sample) off = align256(off + (size_t)p.ksplit * B * kSampleTarget * 4);
+    if (p.sample) off = align256(off + (size_t)p.ksplit * B * p.nsamp * 4);
     p.off_list = off;
     off = align256(off + (size_t)B * p.list_cap * 8);
     p.off_lcnt = off;
@@ -246,8 +249,9 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         sl.nbc = (int)p.nbc;
         sl.samp_log2 = p.samp_log2;
         sl.ksplit = p.ksplit;
+        sl.nsamp = p.nsamp;
         sl.P = P;
-        const int grid = (int)(p.nbc * (kSampleTarget / kTileLatents) * p.ksplit);
+        const int grid = (int)(p.nbc * (p.nsamp / kTileLatents) * p.ksplit);
         int pi = prof_begin("sample_kernel", st);
         e = launch_mainl_sample(dt, sl, grid, st);
         prof_end(pi, st);
@@ -256,9 +260,10 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         SampleArgs sa;
         sa.X = X; sa.W = W; sa.bias = b; sa.B = B; sa.d = d;
         sa.samp_log2 = p.samp_log2;
+        sa.nsamp = p.nsamp;
         sa.P = P;
         int pi = prof_begin("sample_kernel", st);
-        e = launch_sample(dt, sa, dim3((unsigned)(kSampleTarget / 32), (unsigned)cdiv(B, 32)), st);
+        e = launch_sample(dt, sa, dim3((unsigned)(p.nsamp / 32), (unsigned)cdiv(B, 32)), st);
         prof_end(pi, st);
         if (e != hipSuccess) return hip_fail(e, "sample_kernel launch");
     }
@@ -266,7 +271,7 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     ta.P = P;
     ta.nsplit = p.large ? p.ksplit : 1;
     ta.bias = p.large ? b : nullptr;   // sample_kernel adds the bias itself
-    ta.samp_log2 = p.samp_log2; ta.k = (int)k;
+    ta.samp_log2 = p.samp_log2; ta.nsamp = p.nsamp; ta.k = (int)k;
     ta.thr = thr; ta.list_keys = list_keys; ta.list_cnt = list_cnt; ta.list_cap = p.list_cap;
     int pt = prof_begin("thr_kernel", st);
     e = launch_thr(ta, B, st);
@@ -283,6 +288,7 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         ml.thr0 = thr;
         ml.sampled = p.sample ? 1 : 0;
         ml.samp_log2 = p.samp_log2;
+        ml.samp_blocks = p.nsamp / kSampleBlock;
         ml.list_keys = list_keys; ml.list_cap = p.list_cap; ml.head_span = p.head_span;
         ml.seg_cnt = (int32_t*)(ws + p.off_seg);
         int pm = prof_begin("main_kernel", st);
@@ -299,6 +305,7 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         ma.thr0 = thr;
         ma.sampled = p.sample ? 1 : 0;
         ma.samp_log2 = p.samp_log2;
+        ma.samp_blocks = p.nsamp / kSampleBlock;
         ma.list_keys = list_keys; ma.list_cnt = list_cnt; ma.list_cap = p.list_cap;
         int pm = prof_begin("main_kernel", st);
         e = launch_main(dt, p.NB, ma, dim3((unsigned)p.nwg, (unsigned)p.nbc), st);

@@ -11,22 +11,23 @@ constexpr int kTileLatents = 32 * kMainWaves;   // latents per main_kernel tile
 constexpr int kApproxGroup = 128;    // latent group of the approximate variant
 constexpr int kGroupTile = 256;      // latents per group_kernel tile (two groups)
 constexpr int kSampleTarget = 4096;  // sampled latents that seed the thresholds
+constexpr int kSampleLarge = 8192;   //   (large batches with F >= kSampleLargeMinF)
 constexpr int kSampleBlock = 128;    // consecutive latents per sampled block
-constexpr int kSampleBlocks = kSampleTarget / kSampleBlock;
 constexpr int64_t kSampleMinF = 16384;
+constexpr int64_t kSampleLargeMinF = 65536;
 
-// Sampled latent i (0 <= i < kSampleTarget) is latent
-// (i / kSampleBlock) << blk_log2 + i % kSampleBlock: kSampleBlocks blocks of
-// consecutive latents spread evenly over F.
+// Sampled latent i (0 <= i < nsamp) is latent
+// (i / kSampleBlock) << blk_log2 + i % kSampleBlock: nsamp / kSampleBlock
+// blocks of consecutive latents spread evenly over F.
 __host__ __device__ inline int64_t sample_latent(int64_t i, int blk_log2)
 {
     return ((i / kSampleBlock) << blk_log2) + (i % kSampleBlock);
 }
 
-// Whether latent f belongs to the sample.
-__host__ __device__ inline bool is_sampled(int64_t f, int blk_log2)
+// Whether latent f belongs to a sample of `nblocks` blocks.
+__host__ __device__ inline bool is_sampled(int64_t f, int blk_log2, int nblocks)
 {
-    return (f & ((int64_t(1) << blk_log2) - 1)) < kSampleBlock && (f >> blk_log2) < kSampleBlocks;
+    return (f & ((int64_t(1) << blk_log2) - 1)) < kSampleBlock && (f >> blk_log2) < nblocks;
 }
 
 struct MainArgs {
@@ -38,10 +39,10 @@ struct MainArgs {
     int64_t num_tiles, tiles_per_wg;
     const uint64_t* thr0;        // per-row starting threshold keys, or null
     int sampled;                 // non-zero: the sampled latents (is_sampled) were
-    int samp_log2;               //   scored by sample_kernel and are skipped here
+    int samp_log2, samp_blocks;  //   scored by the sample pass and are skipped here
     uint64_t* list_keys;         // [B][list_cap]: every workgroup's final queue, appended
     int32_t* list_cnt;           // [B] keys in each row's list (set by thr_kernel)
-    int64_t list_cap;            // kSampleTarget + nwg * cap: room for the sampled keys
+    int64_t list_cap;            // nsamp + nwg * cap: room for the sampled keys
                                  //   and every workgroup's full queue
 };
 
@@ -50,16 +51,16 @@ struct SampleArgs {
     const void* W;
     const float* bias;
     int64_t B, d;
-    int samp_log2;
-    float* P;                    // [B][kSampleTarget] scores of the sampled latents
+    int samp_log2, nsamp;
+    float* P;                    // [B][nsamp] scores of the sampled latents
 };
 
 struct ThrArgs {
     const float* P;              // sampled scores, or null (no sample: threshold 0):
-                                 //   nsplit partial sums [nsplit][B][kSampleTarget]
+                                 //   nsplit partial sums [nsplit][B][nsamp]
     int nsplit;                  //   added in split order, then
     const float* bias;           //   + bias[latent] if non-null
-    int samp_log2, k;
+    int samp_log2, nsamp, k;
     uint64_t* thr;               // [B] row threshold keys
     uint64_t* list_keys;         // [B][list_cap]: receives the sampled keys >= thr
     int32_t* list_cnt;           // [B] set to the number of those keys
@@ -81,14 +82,14 @@ struct MainLArgs {
     int64_t num_tiles, tiles_per_wg;
     int nbc, nr;                 // row blocks, W ranges (grid = nbc * nr)
     const uint64_t* thr0;        // per-row starting threshold keys
-    int sampled, samp_log2;
+    int sampled, samp_log2, samp_blocks;
     uint64_t* list_keys;         // [B][list_cap]: head_span head slots, then nr segments of cap
     int64_t list_cap, head_span;
     int32_t* seg_cnt;            // [B][nr] keys in each segment
     // sample mode (mainl_sample_kernel): 256-latent tiles of the sampled
     // latents, d split in ksplit ranges; raw partial scores to P
-    int ksplit;
-    float* P;                    // [ksplit][B][kSampleTarget]
+    int ksplit, nsamp;
+    float* P;                    // [ksplit][B][nsamp]
 };
 
 // A row's candidates: slots [0, head_span) hold list_cnt[row] keys at their

@@ -1,7 +1,7 @@
 // stk_kernels.hip -- the exact streaming top-k encoder on gfx950.
 //
-//   sample_kernel  : fp32 scores of kSampleTarget sampled latents (32 blocks of
-//                    128 consecutive latents spread over F) for every row.
+//   sample_kernel  : fp32 scores of the sampled latents (blocks of 128
+//                    consecutive latents spread over F) for every row.
 //   thr_kernel     : per row, a threshold key that at least k sampled keys
 //                    reach (the k-th largest of the per-thread maxima), hence a
 //                    lower bound of the row's k-th key; the sampled keys that
@@ -81,13 +81,13 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
         const int64_t fl = tile0 + wave * 32 + h * 4;
         // latents past F or in the sample are never candidates here
         uint32_t vmask = 0xFFFFu;
-        if (tile0 + kTileLatents > F || (a.sampled && (is_sampled(tile0, a.samp_log2) ||
-                                                       is_sampled(tile0 + kTileLatents - 1, a.samp_log2)))) {
+        if (tile0 + kTileLatents > F || (a.sampled && (is_sampled(tile0, a.samp_log2, a.samp_blocks) ||
+                                                       is_sampled(tile0 + kTileLatents - 1, a.samp_log2, a.samp_blocks)))) {
             vmask = 0;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int64_t f = fl + (r >> 2) * 8 + (r & 3);
-                const bool ok = f < F && !(a.sampled && is_sampled(f, a.samp_log2));
+                const bool ok = f < F && !(a.sampled && is_sampled(f, a.samp_log2, a.samp_blocks));
                 vmask |= ok ? (1u << r) : 0u;
             }
         }
@@ -199,7 +199,7 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
 
 // ---------------------------------------------------------------------------
 // sample_kernel: P[row][i] = X[row] . W[f] + b[f], f = sample_latent(i), for
-// the kSampleTarget sampled latents.  A workgroup owns 32 sampled latents x 32
+// the nsamp sampled latents.  A workgroup owns 32 sampled latents x 32
 // rows; its four waves take interleaved quarters of the d-steps and their fp32
 // partial sums are added in a fixed order (deterministic).  Operands are read
 // straight from global memory (W rows once, X rows from L2).
@@ -262,7 +262,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a)
     }
     __syncthreads();
     if (wave == 0 && jok) {
-        float* prow = a.P + j * kSampleTarget;
+        float* prow = a.P + j * a.nsamp;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int64_t ii = ib + (r >> 2) * 8 + h * 4 + (r & 3);
@@ -280,9 +280,9 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a)
 // (kth_of_maxima), so it never exceeds the row's final k-th key; the sampled
 // keys that reach it are written to the list, since main_kernel skips the
 // sampled latents.
+template <int kItems>
 __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
 {
-    constexpr int kItems = kSampleTarget / kThreads;
     __shared__ SelShared S;
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
@@ -290,8 +290,8 @@ __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
         if (tid == 0) { a.thr[row] = 0; a.list_cnt[row] = 0; }
         return;
     }
-    const float* prow = a.P + row * kSampleTarget;
-    const int64_t split_stride = (int64_t)gridDim.x * kSampleTarget;   // B rows per split
+    const float* prow = a.P + row * (kItems * kThreads);
+    const int64_t split_stride = (int64_t)gridDim.x * (kItems * kThreads);   // B rows per split
     float v[kItems];
 #pragma unroll
     for (int t = 0; t < kItems; ++t) v[t] = prow[tid + t * kThreads];
@@ -440,7 +440,12 @@ hipError_t launch_sample(int dt, const SampleArgs& a, dim3 grid, hipStream_t st)
 
 hipError_t launch_thr(const ThrArgs& a, int64_t rows, hipStream_t st)
 {
-    hipLaunchKernelGGL(thr_kernel, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+    if (a.P != nullptr && a.nsamp == kSampleLarge) {
+        hipLaunchKernelGGL(thr_kernel<kSampleLarge / kThreads>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+        return hipGetLastError();
+    }
+    if (a.P != nullptr && a.nsamp != kSampleTarget) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(thr_kernel<kSampleTarget / kThreads>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     return hipGetLastError();
 }
 

@@ -265,14 +265,14 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
 
     // workgroup -> (row block, W range): the row blocks of a W range share an XCD.
     // Sample mode: workgroup -> (row block, sample tile, d range).
-    constexpr int kSampleTiles = kSampleTarget / kLTile;
     int rb, rg, ks = 0;
     {
         const int id = blockIdx.x;
         if (SAMPLE) {
             rb = id % a.nbc;
-            rg = (id / a.nbc) % kSampleTiles;
-            ks = id / (a.nbc * kSampleTiles);
+            const int stiles = a.nsamp / kLTile;
+            rg = (id / a.nbc) % stiles;
+            ks = id / (a.nbc * stiles);
         } else if ((a.nr & 7) == 0) {
             const int slot = id >> 3;
             rb = slot % a.nbc;
@@ -366,7 +366,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
             }
             if (SAMPLE) {
                 // raw partial scores of this d range: P[ks][row][sample index]
-                float* P = a.P + (int64_t)ks * B * kSampleTarget;
+                float* P = a.P + (int64_t)ks * B * a.nsamp;
 #pragma unroll
                 for (int n = 0; n < kLNB; ++n) {
                     const int64_t row = b0 + 32 * n + jl;
@@ -379,7 +379,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                                 f32x4 v;
 #pragma unroll
                                 for (int e = 0; e < 4; ++e) v[e] = acc[fa][n][r4 * 4 + e];
-                                *(f32x4*)(P + row * kSampleTarget + i) = v;
+                                *(f32x4*)(P + row * a.nsamp + i) = v;
                             }
                     }
                 }
@@ -392,8 +392,8 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
             uint32_t vmask[kLFrags];
             {
                 const bool edge = tile0 + kLTile > F ||
-                                  (a.sampled && (is_sampled(tile0, a.samp_log2) ||
-                                                 is_sampled(tile0 + kLTile - 1, a.samp_log2)));
+                                  (a.sampled && (is_sampled(tile0, a.samp_log2, a.samp_blocks) ||
+                                                 is_sampled(tile0 + kLTile - 1, a.samp_log2, a.samp_blocks)));
 #pragma unroll
                 for (int fa = 0; fa < kLFrags; ++fa) {
                     uint32_t m = 0xFFFFu;
@@ -403,7 +403,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
 #pragma unroll
                         for (int r = 0; r < 16; ++r) {
                             const int64_t f = fl + (r >> 2) * 8 + (r & 3);
-                            const bool ok = f < F && !(a.sampled && is_sampled(f, a.samp_log2));
+                            const bool ok = f < F && !(a.sampled && is_sampled(f, a.samp_log2, a.samp_blocks));
                             m |= ok ? (1u << r) : 0u;
                         }
                     }

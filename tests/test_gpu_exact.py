@@ -257,6 +257,7 @@ LARGE = {
     "large_sampled": dict(B=512, d=256, F=20000, k=128),
     "large_unsampled_ragged": dict(B=600, d=128, F=3000, k=16),
     "large_k64": dict(B=1024, d=512, F=40000, k=64),
+    "large_sample8k": dict(B=520, d=128, F=70001, k=128),   # F >= 65536: 8192 sampled latents
 }
 
 
