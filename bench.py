@@ -95,11 +95,11 @@ def copy_calibration(nbytes, steps):
                                            "GBps_rw": round(8 * n / (us * 1e-6) / 1e9, 1)}}), flush=True)
 
 
-def traffic_from_profile(workload):
-    """HBM bytes per main_kernel launch, as recorded by the calibrated PMC
-    summary profiles/main_kernel_<workload>_hbm_traffic.md (a line
+def traffic_from_profile(kernel, workload):
+    """HBM bytes per launch of the streaming kernel, as recorded by the
+    calibrated PMC summary profiles/<kernel>_<workload>_hbm_traffic.md (a line
     `traffic_bytes_per_launch: N`), or None when no such summary exists."""
-    path = os.path.join(ROOT, "profiles", f"main_kernel_{workload}_hbm_traffic.md")
+    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_hbm_traffic.md")
     try:
         with open(path) as fh:
             for line in fh:
@@ -211,8 +211,11 @@ def main():
     else:
         roof = {"bound": "mfma", "achieved": round(tflops_main, 2), "peak": MFMA_PEAK_TFLOPS[dtn],
                 "unit": "TFLOP/s", "frac": round(tflops_main / MFMA_PEAK_TFLOPS[dtn], 4)}
-    roof["kernel"] = main_name
-    roof["traffic"] = traffic_from_profile(args.workload)
+    # batches of 512 rows or more run the large-batch kernel (mainl_kernel);
+    # both are timed under the profile name main_kernel
+    kname = "mainl_kernel" if B >= 512 else "main_kernel"
+    roof["kernel"] = kname
+    roof["traffic"] = traffic_from_profile(kname, args.workload)
     roof["alg_bytes_per_launch"] = alg_main
     roof["avg_launch_us"] = round(main_us, 2)
 
