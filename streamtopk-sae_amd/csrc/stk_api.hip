@@ -115,7 +115,8 @@ struct ExactPlan {
     int nwg;                     // main_kernel: W ranges; mainl_kernel: nr (grid = nbc * nr)
     bool sample;
     int samp_log2, nsamp;        // sampled latents: nsamp / kSampleBlock blocks, 1 << samp_log2 apart
-    int ksplit;                  // large batches: d ranges of the sample pass
+    int ksplit;                  // d ranges (splits) of the sample pass
+    int snb;                     // sample_kernel: 32-row tiles per workgroup
     int64_t list_cap, head_span;
     size_t off_thr, off_P, off_list, off_lcnt, off_seg, total;
 };
@@ -164,11 +165,23 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
     // workgroup per (row block, 256 sampled latents, d range), enough d
     // ranges to fill the device
     p.ksplit = 1;
+    p.snb = 1;
+    const int64_t nds = d / (dtype == STK_DTYPE_F32 ? 32 : 64);
     if (p.large && p.sample) {
         const int64_t wgs = p.nbc * (p.nsamp / kTileLatents);
         int64_t ks = cdiv(ncu, wgs);
-        const int64_t nds = d / (dtype == STK_DTYPE_F32 ? 32 : 64);
         if (ks > nds) ks = nds;
+        if (ks < 1) ks = 1;
+        p.ksplit = (int)ks;
+    } else if (p.sample) {
+        // small batches: sample_kernel, one workgroup per (32 sampled
+        // latents, row block of up to 128 rows, d range); enough d ranges to
+        // give every CU a workgroup, each wave at least one d-step
+        const int64_t bblocks = cdiv(B, 32);
+        p.snb = bblocks >= 3 ? 4 : (int)bblocks;
+        const int64_t wgs = (p.nsamp / 32) * cdiv(B, 32 * p.snb);
+        int64_t ks = cdiv(ncu, wgs);
+        if (ks > nds / kSampleWaves) ks = nds / kSampleWaves;
         if (ks < 1) ks = 1;
         p.ksplit = (int)ks;
     }
@@ -258,19 +271,21 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         if (e != hipSuccess) return hip_fail(e, "sample launch");
     } else if (p.sample) {
         SampleArgs sa;
-        sa.X = X; sa.W = W; sa.bias = b; sa.B = B; sa.d = d;
+        sa.X = X; sa.W = W; sa.B = B; sa.d = d;
         sa.samp_log2 = p.samp_log2;
         sa.nsamp = p.nsamp;
+        sa.nsplit = p.ksplit;
         sa.P = P;
+        const dim3 grid((unsigned)(p.nsamp / 32 * p.ksplit), (unsigned)cdiv(B, 32 * p.snb));
         int pi = prof_begin("sample_kernel", st);
-        e = launch_sample(dt, sa, dim3((unsigned)(p.nsamp / 32), (unsigned)cdiv(B, 32)), st);
+        e = launch_sample(dt, p.snb, sa, grid, st);
         prof_end(pi, st);
         if (e != hipSuccess) return hip_fail(e, "sample_kernel launch");
     }
     ThrArgs ta;
     ta.P = P;
-    ta.nsplit = p.large ? p.ksplit : 1;
-    ta.bias = p.large ? b : nullptr;   // sample_kernel adds the bias itself
+    ta.nsplit = p.ksplit;
+    ta.bias = b;
     ta.samp_log2 = p.samp_log2; ta.nsamp = p.nsamp; ta.k = (int)k;
     ta.thr = thr; ta.list_keys = list_keys; ta.list_cnt = list_cnt; ta.list_cap = p.list_cap;
     int pt = prof_begin("thr_kernel", st);

@@ -46,13 +46,16 @@ struct MainArgs {
                                  //   and every workgroup's full queue
 };
 
+constexpr int kSampleWaves = 8;      // wavefronts per sample_kernel workgroup
+constexpr int kSampleThreads = 64 * kSampleWaves;
+
 struct SampleArgs {
     const void* X;
     const void* W;
-    const float* bias;
     int64_t B, d;
     int samp_log2, nsamp;
-    float* P;                    // [B][nsamp] scores of the sampled latents
+    int nsplit;                  // d ranges (splits) of the sample pass
+    float* P;                    // [nsplit][B][nsamp] partial scores of the sampled latents
 };
 
 struct ThrArgs {
@@ -136,7 +139,7 @@ size_t group_lds_bytes(int NB);
 hipError_t launch_main(int dt, int NB, const MainArgs& a, dim3 grid, hipStream_t st);
 hipError_t launch_mainl(int dt, const MainLArgs& a, int grid, hipStream_t st);
 hipError_t launch_mainl_sample(int dt, const MainLArgs& a, int grid, hipStream_t st);
-hipError_t launch_sample(int dt, const SampleArgs& a, dim3 grid, hipStream_t st);
+hipError_t launch_sample(int dt, int NB, const SampleArgs& a, dim3 grid, hipStream_t st);
 hipError_t launch_thr(const ThrArgs& a, int64_t rows, hipStream_t st);
 hipError_t launch_merge(const MergeArgs& a, int64_t rows, hipStream_t st);
 hipError_t launch_group(int dt, int NB, const GroupArgs& a, dim3 grid, hipStream_t st);

@@ -24,6 +24,28 @@
 
 namespace stk {
 
+// Register r (0..15, varying per lane) of a lane's 16 accumulators, by a
+// four-level tree of bitwise selects: a lane cannot index its own registers
+// (written as masks so the compiler cannot turn the tree back into an
+// indexed array, which would live in scratch memory).
+__device__ __forceinline__ float sel_bit(uint32_t r, uint32_t bit, float hi, float lo)
+{
+    const uint32_t m = 0u - ((r >> bit) & 1u);
+    return __uint_as_float((m & __float_as_uint(hi)) | (~m & __float_as_uint(lo)));
+}
+
+__device__ __forceinline__ float pick16(const f32x16& v, uint32_t r)
+{
+    const float a0 = sel_bit(r, 0, v[1], v[0]), a1 = sel_bit(r, 0, v[3], v[2]);
+    const float a2 = sel_bit(r, 0, v[5], v[4]), a3 = sel_bit(r, 0, v[7], v[6]);
+    const float a4 = sel_bit(r, 0, v[9], v[8]), a5 = sel_bit(r, 0, v[11], v[10]);
+    const float a6 = sel_bit(r, 0, v[13], v[12]), a7 = sel_bit(r, 0, v[15], v[14]);
+    const float b0 = sel_bit(r, 1, a1, a0), b1 = sel_bit(r, 1, a3, a2);
+    const float b2 = sel_bit(r, 1, a5, a4), b3 = sel_bit(r, 1, a7, a6);
+    const float c0 = sel_bit(r, 2, b1, b0), c1 = sel_bit(r, 2, b3, b2);
+    return sel_bit(r, 3, c1, c0);
+}
+
 // ---------------------------------------------------------------------------
 // main_kernel
 // ---------------------------------------------------------------------------
@@ -120,20 +142,18 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
             __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): every per-bit store below may use them
 #pragma unroll
             for (int n = 0; n < NB; ++n) {
-                const uint32_t m = pend[n];
-                if (m == 0) continue;
-                const int j = 32 * n + jl;
-                uint64_t* qj = q + (size_t)j * cap;
-                uint32_t keep = 0;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    if (m >> r & 1u) {
-                        const int slot = base[n] + __builtin_popcount(m & ((1u << r) - 1u));
-                        if (slot < cap)
-                            qj[slot] = make_key(ac[0][n][r], fl + (r >> 2) * 8 + (r & 3));
-                        else
-                            keep |= 1u << r;
-                    }
+                // this lane's survivors only (about 1 in 50 scores), lowest register first
+                uint64_t* qj = q + (size_t)(32 * n + jl) * cap;
+                uint32_t m = pend[n], keep = 0;
+                int slot = base[n];
+                while (m) {
+                    const uint32_t r = (uint32_t)__builtin_ctz(m);
+                    m &= m - 1u;
+                    if (slot < cap)
+                        qj[slot] = make_key(pick16(ac[0][n], r), fl + (r >> 2) * 8 + (r & 3));
+                    else
+                        keep |= 1u << r;
+                    ++slot;
                 }
                 pend[n] = keep;
                 overflow |= keep != 0;
@@ -171,12 +191,13 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
             // drop pending scores that fell below a raised threshold
 #pragma unroll
             for (int n = 0; n < NB; ++n) {
-                if (pend[n] == 0) continue;
                 const uint64_t tk = thr[32 * n + jl];
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    if ((pend[n] >> r & 1u) && !(make_key(ac[0][n][r], fl + (r >> 2) * 8 + (r & 3)) > tk))
-                        pend[n] &= ~(1u << r);
+                uint32_t m = pend[n];
+                while (m) {
+                    const uint32_t r = (uint32_t)__builtin_ctz(m);
+                    m &= m - 1u;
+                    if (!(make_key(pick16(ac[0][n], r), fl + (r >> 2) * 8 + (r & 3)) > tk)) pend[n] &= ~(1u << r);
+                }
             }
         }
     });
@@ -198,76 +219,115 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
 }
 
 // ---------------------------------------------------------------------------
-// sample_kernel: P[row][i] = X[row] . W[f] + b[f], f = sample_latent(i), for
-// the nsamp sampled latents.  A workgroup owns 32 sampled latents x 32
-// rows; its four waves take interleaved quarters of the d-steps and their fp32
-// partial sums are added in a fixed order (deterministic).  Operands are read
-// straight from global memory (W rows once, X rows from L2).
+// sample_kernel: partial sums P[split][row][i] = X[row] . W[f] over the d-steps
+// of one split, f = sample_latent(i), for the nsamp sampled latents (the bias
+// is added by thr_kernel, after the splits).  A workgroup owns 32 sampled
+// latents x 32*NB rows x one d range, so W is read once per row block of up to
+// 128 rows; X comes from L2.  Its eight waves take interleaved d-steps of the
+// range, two at a time; their partial sums are added in a fixed order through
+// LDS, (a0 + a4) + (a1 + a5) + (a2 + a6) + (a3 + a7), and written as whole
+// 128-byte row segments.
 // ---------------------------------------------------------------------------
-template <int DT>
-__global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a)
+constexpr int kSampleStride = 36;   // floats per LDS-staged row: 32 latents + pad (16-byte aligned)
+
+size_t sample_lds_bytes(int NB)
+{
+    return (size_t)4 * 32 * NB * kSampleStride * 4;
+}
+
+template <int DT, int NB>
+__global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a)
 {
     constexpr int ES = Dt<DT>::esize;
     constexpr int DS = Dt<DT>::DS;
-    __shared__ float red[kWaves - 1][16][64 + 1];
+    constexpr int BT = 32 * NB;
+    constexpr int SW = kSampleWaves;
+    extern __shared__ __align__(16) unsigned char smem[];
+    float* T = (float*)smem;   // [4][BT][kSampleStride]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, jl = lane & 31;
-    const int64_t ib = (int64_t)blockIdx.x * 32;
-    const int64_t jb = (int64_t)blockIdx.y * 32;
+    const int nlb = a.nsamp / 32;
+    const int lb = (int)(blockIdx.x % nlb);
+    const int sp = (int)(blockIdx.x / nlb);
+    const int64_t ib = (int64_t)lb * 32;
+    const int64_t b0 = (int64_t)blockIdx.y * BT;
     const int64_t d = a.d;
     const int64_t nds = d / DS;   // d is a whole number of steps (checked on the host)
-
-    // the bias of this lane's output latents, fetched first: stores to P could
-    // alias it, so it must not be read after them
-    float bias_r[16];
-    if (wave == 0) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-            bias_r[r] = a.bias[sample_latent(ib + (r >> 2) * 8 + h * 4 + (r & 3), a.samp_log2)];
-    }
+    const int64_t sb = sp * nds / a.nsplit, se = (sp + 1) * nds / a.nsplit;
 
     const unsigned char* wp = (const unsigned char*)a.W + sample_latent(ib + jl, a.samp_log2) * d * ES + h * 64;
-    const int64_t j = jb + jl;
-    const bool jok = j < a.B;
-    // rows past B read row 0; their sums are never stored
-    const unsigned char* xp = (const unsigned char*)a.X + (jok ? j : 0) * d * ES + h * 64;
+    const unsigned char* xp[NB];
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+        // rows past B read row 0; their sums are never stored
+        const int64_t j = b0 + 32 * n + jl;
+        xp[n] = (const unsigned char*)a.X + (j < a.B ? j : 0) * d * ES + h * 64;
+    }
 
-    f32x16 acc;
+    f32x16 acc[NB];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-    for (int64_t s0 = wave; s0 < nds; s0 += 4 * kWaves) {
-        u32x4 wq[4][4], xq[4][4];
+    for (int n = 0; n < NB; ++n)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int64_t s = s0 + t * kWaves;
-            const int64_t sc = s < nds ? s : nds - 1;   // in bounds; zeroed below
+        for (int r = 0; r < 16; ++r) acc[n][r] = 0.f;
+    for (int64_t s0 = sb + wave; s0 < se; s0 += 2 * SW) {
+        u32x4 wq[2][4], xq[2][NB][4];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int64_t s = s0 + t * SW;
+            const int64_t sc = s < se ? s : s0;   // in bounds; its W is zeroed below
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 wq[t][q] = *(const u32x4*)(wp + sc * kStepBytes + q * 16);
-                xq[t][q] = *(const u32x4*)(xp + sc * kStepBytes + q * 16);
+#pragma unroll
+                for (int n = 0; n < NB; ++n) xq[t][n][q] = *(const u32x4*)(xp[n] + sc * kStepBytes + q * 16);
             }
-            if (s >= nds) {
+            if (s >= se) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) wq[t][q] = u32x4{0u, 0u, 0u, 0u};
             }
         }
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) mfma_quad<DT>(acc, wq[t][q], xq[t][q]);
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int n = 0; n < NB; ++n) mfma_quad<DT>(acc[n], wq[t][q], xq[t][n][q]);
     }
-    if (wave > 0) {
+
+    // registers 4g..4g+3 of a lane hold latents 8g + 4h + 0..3 of row 32n + jl
+    auto stage = [&](float* buf) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) red[wave - 1][r][lane] = acc[r];
+        for (int n = 0; n < NB; ++n)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *(f32x4*)(buf + (32 * n + jl) * kSampleStride + 8 * g + 4 * h) =
+                    f32x4{acc[n][4 * g], acc[n][4 * g + 1], acc[n][4 * g + 2], acc[n][4 * g + 3]};
+    };
+    if (wave >= 4) stage(T + (wave - 4) * BT * kSampleStride);
+    __syncthreads();
+    if (wave < 4) {
+        float* buf = T + wave * BT * kSampleStride;
+#pragma unroll
+        for (int n = 0; n < NB; ++n)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 v = *(const f32x4*)(buf + (32 * n + jl) * kSampleStride + 8 * g + 4 * h);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[n][4 * g + e] += v[e];
+            }
+        stage(buf);
     }
     __syncthreads();
-    if (wave == 0 && jok) {
-        float* prow = a.P + j * a.nsamp;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t ii = ib + (r >> 2) * 8 + h * 4 + (r & 3);
-            const float s = ((acc[r] + red[0][r][lane]) + red[1][r][lane]) + red[2][r][lane];
-            prow[ii] = s + bias_r[r];
+    float* Ps = a.P + (int64_t)sp * a.B * a.nsamp;
+    for (int c = tid; c < BT * 8; c += kSampleThreads) {
+        const int row = c >> 3, c4 = (c & 7) * 4;
+        const int64_t j = b0 + row;
+        if (j < a.B) {
+            const float* t0 = T + row * kSampleStride + c4;
+            constexpr int WS = BT * kSampleStride;
+            const f32x4 v = ((*(const f32x4*)t0 + *(const f32x4*)(t0 + WS)) + *(const f32x4*)(t0 + 2 * WS)) +
+                            *(const f32x4*)(t0 + 3 * WS);
+            *(f32x4*)(Ps + j * a.nsamp + ib + c4) = v;
         }
     }
 }
@@ -429,13 +489,26 @@ hipError_t launch_main(int dt, int NB, const MainArgs& a, dim3 grid, hipStream_t
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_sample(int dt, const SampleArgs& a, dim3 grid, hipStream_t st)
+template <int DT, int NB>
+static hipError_t launch_sample_t(const SampleArgs& a, dim3 grid, hipStream_t st)
 {
-    if (dt == DT_BF16) hipLaunchKernelGGL(sample_kernel<DT_BF16>, grid, dim3(kThreads), 0, st, a);
-    else if (dt == DT_F16) hipLaunchKernelGGL(sample_kernel<DT_F16>, grid, dim3(kThreads), 0, st, a);
-    else if (dt == DT_F32) hipLaunchKernelGGL(sample_kernel<DT_F32>, grid, dim3(kThreads), 0, st, a);
-    else return hipErrorInvalidValue;
+    const size_t lds = sample_lds_bytes(NB);
+    auto kern = sample_kernel<DT, NB>;
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, grid, dim3(kSampleThreads), lds, st, a);
     return hipGetLastError();
+}
+
+hipError_t launch_sample(int dt, int NB, const SampleArgs& a, dim3 grid, hipStream_t st)
+{
+#define STK_CASE(DTV, NBV) \
+    if (dt == DTV && NB == NBV) return launch_sample_t<DTV, NBV>(a, grid, st);
+    STK_CASE(DT_BF16, 1) STK_CASE(DT_BF16, 2) STK_CASE(DT_BF16, 4)
+    STK_CASE(DT_F16, 1) STK_CASE(DT_F16, 2) STK_CASE(DT_F16, 4)
+    STK_CASE(DT_F32, 1) STK_CASE(DT_F32, 2) STK_CASE(DT_F32, 4)
+#undef STK_CASE
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_thr(const ThrArgs& a, int64_t rows, hipStream_t st)
