@@ -90,11 +90,13 @@ int stk_cpu_forward(const float* X, const float* W, const float* b, float* V, in
                     int64_t B, int64_t d, int64_t F, int64_t k, int num_threads);
 
 /* Per-kernel timing (no counterpart in the reference; used by bench.py).
- * While enabled, every device entry point called on this thread records a HIP
- * event pair on its stream around the kernels it launches: every kernel for
- * on=1, only the streaming kernels (main_kernel, group_kernel) for on=2, so
- * that timing a loop adds no events between the other kernels.  Enabling
- * discards earlier records; on=0 stops recording and frees the events. */
+ * While enabled, every device entry point called on this thread records the
+ * start and end of the kernels it launches with a HIP event pair carried in
+ * each kernel's own dispatch packet (hipExtLaunchKernelGGL), which adds no
+ * work or idle time between kernels: every kernel for on=1, only the
+ * streaming kernels (main_kernel, mainl_kernel, group_kernel; read back as
+ * "main_kernel" / "group_kernel") for on=2.  Enabling discards earlier
+ * records; on=0 stops recording and frees the events. */
 int stk_profile_enable(int on);
 
 /* Total milliseconds and number of launches recorded for `kernel`

@@ -62,20 +62,38 @@ static hipEvent_t prof_event()
     return e;
 }
 
-static int prof_begin(const char* name, hipStream_t st)
+LaunchEvents& launch_events()
+{
+    static thread_local LaunchEvents ev;
+    return ev;
+}
+
+// Arms the next kernel launch to record a start/stop event pair (in its own
+// dispatch packet) under `name`.
+static int prof_begin(const char* name, hipStream_t)
 {
     if (!g_prof) return -1;
     if (g_prof == 2 && std::strcmp(name, "main_kernel") != 0 && std::strcmp(name, "group_kernel") != 0) return -1;
     ProfRec r{name, prof_event(), prof_event()};
     if (!r.a || !r.b) return -1;
-    (void)hipEventRecord(r.a, st);
+    launch_events() = LaunchEvents{r.a, r.b};
     g_recs.push_back(r);
     return (int)g_recs.size() - 1;
 }
 
-static void prof_end(int idx, hipStream_t st)
+// Disarms the events if the launch did not take them (it failed first): the
+// record is dropped so reading it cannot wait on an event never recorded.
+static void prof_end(int idx, hipStream_t)
 {
-    if (idx >= 0 && idx < (int)g_recs.size()) (void)hipEventRecord(g_recs[idx].b, st);
+    LaunchEvents& ev = launch_events();
+    if (ev.start != nullptr) {
+        ev = LaunchEvents{};
+        if (idx >= 0 && idx + 1 == (int)g_recs.size()) {
+            g_pool.push_back(g_recs.back().a);
+            g_pool.push_back(g_recs.back().b);
+            g_recs.pop_back();
+        }
+    }
 }
 
 static void prof_release()

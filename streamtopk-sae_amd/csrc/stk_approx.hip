@@ -179,7 +179,7 @@ static hipError_t launch_group_t(const GroupArgs& a, dim3 grid, hipStream_t st)
     auto kern = group_kernel<DT, NB>;
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, st, a);
+    launch(kern, grid, dim3(kThreads), lds, st, a);
     return hipGetLastError();
 }
 
@@ -196,7 +196,7 @@ hipError_t launch_group(int dt, int NB, const GroupArgs& a, dim3 grid, hipStream
 
 hipError_t launch_cand(const CandArgs& a, int64_t rows, hipStream_t st)
 {
-    hipLaunchKernelGGL(cand_kernel, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+    launch(cand_kernel, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     return hipGetLastError();
 }
 

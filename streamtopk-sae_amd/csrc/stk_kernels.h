@@ -1,9 +1,32 @@
 // stk_kernels.h -- kernel argument blocks and host launch helpers shared by
 // the kernels (stk_kernels.hip, stk_approx.hip) and the C ABI (stk_api.hip).
 #pragma once
+#include <hip/hip_ext.h>
 #include "stk_select.h"
 
 namespace stk {
+
+// Events the next kernel launch of this thread records at the kernel's start
+// and end, or null.  They ride in the kernel's dispatch packet
+// (hipExtLaunchKernelGGL), so timing adds no packets, and no idle time,
+// between kernels.
+struct LaunchEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+LaunchEvents& launch_events();
+
+// Every kernel of the library is launched through here.
+template <class K, class... A>
+inline void launch(K kern, dim3 grid, dim3 block, size_t lds, hipStream_t st, A... args)
+{
+    LaunchEvents& ev = launch_events();
+    if (ev.start != nullptr) {
+        hipExtLaunchKernelGGL(kern, grid, block, (uint32_t)lds, st, ev.start, ev.stop, 0u, args...);
+        ev = LaunchEvents{};
+    } else {
+        hipLaunchKernelGGL(kern, grid, block, lds, st, args...);
+    }
+}
 
 constexpr int kMainWaves = 8;        // wavefronts per main_kernel workgroup (2 per SIMD)
 constexpr int kMainThreads = 64 * kMainWaves;

@@ -2,10 +2,9 @@
 //
 //   sample_kernel  : fp32 scores of the sampled latents (blocks of 128
 //                    consecutive latents spread over F) for every row.
-//   thr_kernel     : per row, a threshold key that at least k sampled keys
-//                    reach (the k-th largest of the per-thread maxima), hence a
-//                    lower bound of the row's k-th key; the sampled keys that
-//                    reach it open the row's candidate list.
+//   thr_kernel     : per row, the k-th largest sampled key: a lower bound of
+//                    the row's k-th key; the sample's top k open the row's
+//                    candidate list.
 //   main_kernel    : streams W once; MFMA scores for 256 latents x up to 128
 //                    rows per tile (the sampled latents are skipped: each latent
 //                    is scored by exactly one kernel); scores not below the
@@ -63,7 +62,11 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
     uint64_t* q = (uint64_t*)(smem + 3 * BT * kXRowStride);
     const int cap = a.cap;
     uint64_t* thr = q + (size_t)BT * cap;
-    int* cnt = (int*)(thr + BT);
+    // queue fill counts, 16 bits per row: word jl holds rows 32n + jl at bits
+    // 16n, so one 64-bit LDS atomic reserves a lane's slots in all its rows
+    uint64_t* cnt64 = thr + BT;
+    uint16_t* cnt = (uint16_t*)cnt64;
+    auto ci = [](int row) { return 4 * (row & 31) + (row >> 5); };
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, jl = lane & 31;
@@ -71,10 +74,9 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
     const int64_t B = a.B, F = a.F;
     const int k = a.k;
 
-    for (int i = tid; i < BT; i += kMainThreads) {
-        cnt[i] = 0;
+    for (int i = tid; i < BT; i += kMainThreads)
         thr[i] = (a.thr0 != nullptr && b0 + i < B) ? a.thr0[b0 + i] : 0ull;
-    }
+    if (tid < 32) cnt64[tid] = 0;
 
     TileStream<DT, NB, FRAGS, WAVES> ts;
     ts.W = (const unsigned char*)a.W;
@@ -135,11 +137,14 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
         for (int it = 0; it < 4096; ++it) {
             bool overflow = false;
             // reserve the slots of every row block first, then wait once
+            uint64_t add = 0;
+#pragma unroll
+            for (int n = 0; n < NB; ++n) add |= (uint64_t)__builtin_popcount(pend[n]) << (16 * n);
+            // a field never carries into the next: counts stay below cap + 512
+            const uint64_t old = add ? atomicAdd((unsigned long long*)&cnt64[jl], (unsigned long long)add) : 0ull;
             int base[NB];
 #pragma unroll
-            for (int n = 0; n < NB; ++n)
-                base[n] = pend[n] ? atomicAdd(&cnt[32 * n + jl], __builtin_popcount(pend[n])) : 0;
-            __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): every per-bit store below may use them
+            for (int n = 0; n < NB; ++n) base[n] = (int)((old >> (16 * n)) & 0xFFFFu);
 #pragma unroll
             for (int n = 0; n < NB; ++n) {
                 // this lane's survivors only (about 1 in 50 scores), lowest register first
@@ -162,7 +167,7 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
             // wave w compacts its rows w*kRowsPerWave + i whose queue is full
             {
                 const int myrow = wave * kRowsPerWave + (lane < kRowsPerWave ? lane : 0);
-                uint64_t full = __ballot(lane < kRowsPerWave && cnt[myrow] >= cap);
+                uint64_t full = __ballot(lane < kRowsPerWave && cnt[ci(myrow)] >= cap);
                 while (full) {
                     const int i = __builtin_ctzll(full);
                     full &= full - 1;
@@ -184,7 +189,7 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
                             if (rk[mm] == k - 1) thr[row] = e[mm];
                         }
                     }
-                    if (lane == 0) cnt[row] = k;
+                    if (lane == 0) cnt[ci(row)] = (uint16_t)k;
                 }
             }
             __syncthreads();
@@ -206,14 +211,14 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
     __syncthreads();
     int* lbase = (int*)thr;   // the thresholds are no longer needed
     for (int i = tid; i < BT; i += kMainThreads) {
-        const int c = (b0 + i < B) ? (cnt[i] < cap ? cnt[i] : cap) : 0;
-        cnt[i] = c;
+        const int c = (b0 + i < B) ? (cnt[ci(i)] < cap ? cnt[ci(i)] : cap) : 0;
+        cnt[ci(i)] = (uint16_t)c;
         lbase[i] = c ? atomicAdd(&a.list_cnt[b0 + i], c) : 0;
     }
     __syncthreads();
     for (int idx = tid; idx < BT * cap; idx += kMainThreads) {
         const int row = idx / cap, e = idx - row * cap;
-        if (e < cnt[row])
+        if (e < cnt[ci(row)])
             a.list_keys[(size_t)(b0 + row) * a.list_cap + lbase[row] + e] = q[(size_t)row * cap + e];
     }
 }
@@ -336,10 +341,10 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a)
 // Selection kernels (one workgroup per row).
 // ---------------------------------------------------------------------------
 // Per row: the threshold key main_kernel starts from and the head of the
-// row's candidate list.  At least k sampled keys are >= the threshold
-// (kth_of_maxima), so it never exceeds the row's final k-th key; the sampled
-// keys that reach it are written to the list, since main_kernel skips the
-// sampled latents.
+// row's candidate list.  The threshold is the k-th largest sampled key (k
+// real scores reach it, so it never exceeds the row's final k-th key); the
+// sampled keys that reach it -- the sample's top k -- are written to the
+// list, since main_kernel skips the sampled latents.
 template <int kItems>
 __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
 {
@@ -370,20 +375,54 @@ __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
         key[t] = make_key(v[t], sample_latent(tid + t * kThreads, a.samp_log2));
         m = key[t] > m ? key[t] : m;
     }
-    if (tid == 0) S.cnt = 0;
-    const uint64_t T = kth_of_maxima(S, m, a.k, tid);
+    if (tid == 0) { S.cnt = 0; S.sel_cnt = 0; }
+    // T0 <= the sample's k-th key; the keys that reach it are few (about
+    // 2-4% of the sample) and include the sample's k largest, whose k-th key
+    // is the threshold: a lower bound of the row's k-th key (k real scores
+    // reach it) and the tightest one the sample gives.
+    const uint64_t T0 = kth_of_maxima(S, m, a.k, tid);
     uint32_t pass = 0;
 #pragma unroll
-    for (int t = 0; t < kItems; ++t) pass |= (key[t] >= T) ? (1u << t) : 0u;
-    const int base = pass ? atomicAdd(&S.cnt, __builtin_popcount(pass)) : 0;
-    uint64_t* out = a.list_keys + row * a.list_cap;
+    for (int t = 0; t < kItems; ++t) pass |= (key[t] >= T0) ? (1u << t) : 0u;
+    const int base = wave_reserve(&S.cnt, __builtin_popcount(pass));
 #pragma unroll
-    for (int t = 0; t < kItems; ++t)
-        if (pass >> t & 1u) out[base + __builtin_popcount(pass & ((1u << t) - 1u))] = key[t];
+    for (int t = 0; t < kItems; ++t) {
+        const int pos = base + __builtin_popcount(pass & ((1u << t) - 1u));
+        if ((pass >> t & 1u) && pos < kSelCap) S.buf[pos] = key[t];
+    }
+    __syncthreads();
+    const int n = S.cnt;   // >= k: at least k sampled keys reach T0
+    uint64_t T = T0;
+    uint64_t* out = a.list_keys + row * a.list_cap;
+    if (n <= kThreads) {
+        // the sample's k largest keys, sorted: the k-th is the threshold
+        const uint64_t v = bitonic_desc(S, tid < n ? S.buf[tid] : 0ull, tid);
+        if (tid == a.k - 1) S.thr = v;
+        if (tid < a.k) out[tid] = v;
+        if (tid == 0) S.sel_cnt = a.k;
+        __syncthreads();
+        T = S.thr;
+    } else if (n <= kSelCap) {
+        for (int i0 = 0; i0 < n; i0 += kThreads) {
+            const int i = i0 + tid;
+            const uint64_t kk = i < n ? S.buf[i] : 0ull;
+            const bool f = i < n && kk >= T;
+            const int pos = wave_reserve1(&S.sel_cnt, f);
+            if (f) out[pos] = kk;
+        }
+    } else {
+        uint32_t hit = 0;
+#pragma unroll
+        for (int t = 0; t < kItems; ++t) hit |= (key[t] >= T) ? (1u << t) : 0u;
+        const int hb = wave_reserve(&S.sel_cnt, __builtin_popcount(hit));
+#pragma unroll
+        for (int t = 0; t < kItems; ++t)
+            if (hit >> t & 1u) out[hb + __builtin_popcount(hit & ((1u << t) - 1u))] = key[t];
+    }
     __syncthreads();
     if (tid == 0) {
         a.thr[row] = T;
-        a.list_cnt[row] = S.cnt;
+        a.list_cnt[row] = S.sel_cnt;
     }
 }
 
@@ -432,10 +471,12 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
         for (int u = 0; u < kPer; ++u) pend |= (v[u] != 0 && v[u] >= thr) ? (1u << u) : 0u;
         for (;;) {
             bool stalled = false;
+            const uint32_t pm = pend;
+            const int base = wave_reserve(&S.cnt, __builtin_popcount(pm));
 #pragma unroll
             for (int u = 0; u < kPer; ++u) {
-                if (pend >> u & 1u) {
-                    const int pos = atomicAdd(&S.cnt, 1);
+                if (pm >> u & 1u) {
+                    const int pos = base + __builtin_popcount(pm & ((1u << u) - 1u));
                     if (pos < kSelCap) {
                         S.buf[pos] = v[u];
                         pend &= ~(1u << u);
@@ -464,7 +505,7 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
 size_t main_lds_bytes(int NB, int cap)
 {
     const size_t BT = 32 * (size_t)NB;
-    return 3 * BT * kXRowStride + BT * (size_t)cap * 8 + BT * 8 + BT * 4;
+    return 3 * BT * kXRowStride + BT * (size_t)cap * 8 + BT * 8 + 32 * 8;
 }
 
 template <int DT, int NB>
@@ -474,7 +515,7 @@ static hipError_t launch_main_t(const MainArgs& a, dim3 grid, hipStream_t st)
     auto kern = main_kernel<DT, NB>;
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kern, grid, dim3(kMainThreads), lds, st, a);
+    launch(kern, grid, dim3(kMainThreads), lds, st, a);
     return hipGetLastError();
 }
 
@@ -496,7 +537,7 @@ static hipError_t launch_sample_t(const SampleArgs& a, dim3 grid, hipStream_t st
     auto kern = sample_kernel<DT, NB>;
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kern, grid, dim3(kSampleThreads), lds, st, a);
+    launch(kern, grid, dim3(kSampleThreads), lds, st, a);
     return hipGetLastError();
 }
 
@@ -514,17 +555,17 @@ hipError_t launch_sample(int dt, int NB, const SampleArgs& a, dim3 grid, hipStre
 hipError_t launch_thr(const ThrArgs& a, int64_t rows, hipStream_t st)
 {
     if (a.P != nullptr && a.nsamp == kSampleLarge) {
-        hipLaunchKernelGGL(thr_kernel<kSampleLarge / kThreads>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+        launch(thr_kernel<kSampleLarge / kThreads>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
         return hipGetLastError();
     }
     if (a.P != nullptr && a.nsamp != kSampleTarget) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(thr_kernel<kSampleTarget / kThreads>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+    launch(thr_kernel<kSampleTarget / kThreads>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     return hipGetLastError();
 }
 
 hipError_t launch_merge(const MergeArgs& a, int64_t rows, hipStream_t st)
 {
-    hipLaunchKernelGGL(merge_kernel, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+    launch(merge_kernel, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     return hipGetLastError();
 }
 

@@ -524,7 +524,7 @@ static hipError_t launch_mainl_t(const MainLArgs& a, int grid, hipStream_t st)
     auto kern = mainl_kernel<DT, SAMPLE>;
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kLargeThreads), lds, st, a);
+    launch(kern, dim3((unsigned)grid), dim3(kLargeThreads), lds, st, a);
     return hipGetLastError();
 }
 

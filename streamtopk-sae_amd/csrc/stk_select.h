@@ -1,6 +1,7 @@
 // stk_select.h -- workgroup-wide top-k selection over 64-bit sort keys held in
-// LDS (radix select by 8-bit digits, most significant first), plus the rank
-// sort used to emit the final k keys in descending order.
+// LDS (radix select by 8-bit digits, most significant first), the bitonic sort
+// that emits the final k keys in descending order, and slot reservation with
+// one LDS atomic per wave.
 #pragma once
 #include "stk_device.h"
 
@@ -14,36 +15,84 @@ struct SelShared {
     uint32_t hist[kWaves][256];
     uint64_t sel[kMaxK];
     uint64_t tmax[kThreads];
+    uint64_t wthr[kWaves];
     uint64_t prefix, mask, thr;
     uint32_t remaining;
     int cnt, sel_cnt, done;
 };
 
-constexpr int kRankMax = 512;   // candidates ranked directly (more -> radix select first)
+// Slots for c >= 0 items of each lane from the LDS counter *ctr, with one
+// atomic per wave (same-address LDS atomics serialise lane by lane): returns
+// the lane's first slot; the wave's slots are in lane order.  Every lane of
+// the wave must take part.
+__device__ inline int wave_reserve(int* ctr, int c)
+{
+    const int lane = (int)__lane_id();
+    int x = c;   // inclusive scan over the lanes
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(x, off, 64);
+        if (lane >= off) x += t;
+    }
+    const int total = __shfl(x, 63, 64);
+    int base = 0;
+    if (lane == 0 && total > 0) base = atomicAdd(ctr, total);
+    return __shfl(base, 0, 64) + x - c;
+}
+
+// wave_reserve for one item per flagged lane.
+__device__ inline int wave_reserve1(int* ctr, bool f)
+{
+    const uint64_t b = __ballot(f);
+    const int pre = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+    int base = 0;
+    if (__lane_id() == 0 && b != 0) base = atomicAdd(ctr, __popcll(b));
+    return __shfl(base, 0, 64) + pre;
+}
 
 // Every thread passes the largest key it holds (0 if none).  Returns a key T
-// such that at least min(k, #keys) keys are >= T: the k-th largest of the
-// per-thread maxima (those k maxima are themselves >= T), or 1 (accept every
-// real key) when fewer than k threads hold a key.
+// such that at least k keys are >= T, or 1 (accept every real key) when a
+// wave holds too few keys.  k is split over the waves (k_w = k / kWaves, the
+// first k % kWaves waves one more); wave w's bound is the k_w-th largest of
+// its 64 maxima, which are themselves keys, and T is the smallest bound over
+// the waves with k_w > 0: at least sum k_w = k keys reach T.  Ranking within
+// a wave costs a quarter of ranking all the workgroup's maxima.
 __device__ inline uint64_t kth_of_maxima(SelShared& S, uint64_t m, int k, int tid)
 {
+    const int lane = tid & 63, wave = tid >> 6;
+    const int kw = k / kWaves + (wave < k % kWaves ? 1 : 0);
     S.tmax[tid] = m;
-    if (tid == 0) S.thr = 1;
-    const int nz = __syncthreads_count(m != 0);
-    if (nz < k) return 1;
-    if (m != 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int nz = __popcll(__ballot(m != 0));
+    uint64_t tw = ~0ull;   // no bound from this wave
+    if (kw > 0 && nz < kw) {
+        tw = 1;
+    } else if (kw > 0) {
         int r = 0;
-        for (int i = 0; i < kThreads; i += 16) {
+        const uint64_t* wm = S.tmax + wave * 64;
+#pragma unroll
+        for (int i = 0; i < 64; i += 16) {
             u64x2 v[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = *(const u64x2*)(S.tmax + i + 2 * u);
+            for (int u = 0; u < 8; ++u) v[u] = *(const u64x2*)(wm + i + 2 * u);
 #pragma unroll
             for (int u = 0; u < 8; ++u) r += (int)(v[u][0] > m) + (int)(v[u][1] > m);
         }
-        if (r == k - 1) S.thr = m;
+        // keys are distinct, so exactly one non-zero maximum has rank kw - 1
+        const uint64_t hit = __ballot(m != 0 && r == kw - 1);
+        const int src = __builtin_ctzll(hit);
+        const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)m, src);
+        const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(m >> 32), src);
+        tw = ((uint64_t)hi << 32) | lo;
     }
+    if (lane == 0) S.wthr[wave] = tw;
     __syncthreads();
-    return S.thr;
+    uint64_t T = S.wthr[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) T = S.wthr[w] < T ? S.wthr[w] : T;
+    return T;
 }
 
 // Finds the digit prefix of the k-th largest key among buf[0..n): afterwards
@@ -107,12 +156,12 @@ __device__ inline void select_compact(SelShared& S, int n, int k, int tid)
     const uint64_t prefix = S.prefix, mask = S.mask;
     if (tid == 0) S.sel_cnt = 0;
     __syncthreads();
-    for (int i = tid; i < n; i += kThreads) {
-        const uint64_t key = S.buf[i];
-        if ((key & mask) >= prefix) {
-            const int p = atomicAdd(&S.sel_cnt, 1);
-            if (p < kMaxK) S.sel[p] = key;
-        }
+    for (int i0 = 0; i0 < n; i0 += kThreads) {
+        const int i = i0 + tid;
+        const uint64_t key = i < n ? S.buf[i] : 0ull;
+        const bool f = i < n && (key & mask) >= prefix;
+        const int p = wave_reserve1(&S.sel_cnt, f);
+        if (f && p < kMaxK) S.sel[p] = key;
     }
     __syncthreads();
     if (tid < k) S.buf[tid] = S.sel[tid];
@@ -130,6 +179,37 @@ __device__ inline void select_compact(SelShared& S, int n, int k, int tid)
         if (lane == 0) { S.thr = m; S.cnt = k; }
     }
     __syncthreads();
+}
+
+// Bitonic sort of one key per thread (kThreads keys, padding 0) into
+// descending order: returns the key of rank tid.  Compare-exchange partners
+// closer than a wave apart are reached by lane shuffles; the three farther
+// stages go through S.tmax, with barriers.  Every thread must take part.
+__device__ inline uint64_t bitonic_desc(SelShared& S, uint64_t v, int tid)
+{
+#pragma unroll
+    for (int size = 2; size <= kThreads; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            uint64_t o;
+            if (stride >= 64) {
+                __syncthreads();
+                S.tmax[tid] = v;
+                __syncthreads();
+                o = S.tmax[tid ^ stride];
+            } else {
+                const uint32_t lo = __shfl_xor((uint32_t)v, stride, 64);
+                const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), stride, 64);
+                o = ((uint64_t)hi << 32) | lo;
+            }
+            // blocks of `size` alternate direction; the final one is descending
+            const bool desc = (tid & size) == 0;
+            const bool lower = (tid & stride) == 0;
+            v = (lower == desc) ? (o > v ? o : v) : (o < v ? o : v);
+        }
+    }
+    __syncthreads();   // S.tmax free again
+    return v;
 }
 
 // Rank of `key` among buf[0..n) in descending key order (keys are unique).
@@ -155,17 +235,15 @@ __device__ inline int emit_topk(SelShared& S, int k, int tid, Emit emit)
 {
     __syncthreads();
     int n = S.cnt < kSelCap ? S.cnt : kSelCap;
-    if (n > kRankMax) {
-        select_compact(S, n, k, tid);
+    if (n > kThreads) {
+        select_compact(S, n, k, tid);   // k <= kMaxK <= kThreads keys remain
         n = k;
     }
     __syncthreads();
-    for (int i = tid; i < n; i += kThreads) {
-        const uint64_t key = S.buf[i];
-        const int r = rank_desc(S, n, key);
-        if (r < k) emit(r, key);
-    }
-    return n < k ? n : k;
+    const uint64_t v = bitonic_desc(S, tid < n ? S.buf[tid] : 0ull, tid);
+    const int m = n < k ? n : k;
+    if (tid < m) emit(tid, v);
+    return m;
 }
 
 }  // namespace stk
