@@ -192,15 +192,15 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
         if (ks < 1) ks = 1;
         p.ksplit = (int)ks;
     } else if (p.sample) {
-        // small batches: sample_kernel, one workgroup per (32 sampled
-        // latents, row block of up to 128 rows, d range); enough d ranges to
-        // give every CU a workgroup, each wave at least one d-step
+        // small batches: sample_kernel, one workgroup per (64 sampled
+        // latents, row block of up to 128 rows, d range of at most
+        // kSampleSteps steps); more d ranges while that leaves CUs idle
         const int64_t bblocks = cdiv(B, 32);
         p.snb = bblocks >= 3 ? 4 : (int)bblocks;
-        const int64_t wgs = (p.nsamp / 32) * cdiv(B, 32 * p.snb);
+        const int64_t wgs = (p.nsamp / kSampleLat) * cdiv(B, 32 * p.snb);
         int64_t ks = cdiv(ncu, wgs);
-        if (ks > nds / kSampleWaves) ks = nds / kSampleWaves;
-        if (ks < 1) ks = 1;
+        if (ks > nds) ks = nds;
+        if (ks < cdiv(nds, kSampleSteps)) ks = cdiv(nds, kSampleSteps);
         p.ksplit = (int)ks;
     }
     p.head_span = p.sample ? p.nsamp : 0;
@@ -294,7 +294,7 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         sa.nsamp = p.nsamp;
         sa.nsplit = p.ksplit;
         sa.P = P;
-        const dim3 grid((unsigned)(p.nsamp / 32 * p.ksplit), (unsigned)cdiv(B, 32 * p.snb));
+        const dim3 grid((unsigned)(p.nsamp / kSampleLat * p.ksplit), (unsigned)cdiv(B, 32 * p.snb));
         int pi = prof_begin("sample_kernel", st);
         e = launch_sample(dt, p.snb, sa, grid, st);
         prof_end(pi, st);

@@ -71,6 +71,8 @@ struct MainArgs {
 
 constexpr int kSampleWaves = 8;      // wavefronts per sample_kernel workgroup
 constexpr int kSampleThreads = 64 * kSampleWaves;
+constexpr int kSampleSteps = 8;      // d-steps per sample_kernel workgroup (at most)
+constexpr int kSampleLat = 64;       // sampled latents per sample_kernel workgroup
 
 struct SampleArgs {
     const void* X;

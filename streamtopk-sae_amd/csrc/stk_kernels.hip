@@ -226,18 +226,22 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
 // ---------------------------------------------------------------------------
 // sample_kernel: partial sums P[split][row][i] = X[row] . W[f] over the d-steps
 // of one split, f = sample_latent(i), for the nsamp sampled latents (the bias
-// is added by thr_kernel, after the splits).  A workgroup owns 32 sampled
-// latents x 32*NB rows x one d range, so W is read once per row block of up to
-// 128 rows; X comes from L2.  Its eight waves take interleaved d-steps of the
-// range, two at a time; their partial sums are added in a fixed order through
-// LDS, (a0 + a4) + (a1 + a5) + (a2 + a6) + (a3 + a7), and written as whole
-// 128-byte row segments.
+// is added by thr_kernel, after the splits).  A workgroup owns 64 sampled
+// latents x 32*NB rows x one d range of at most kSampleSteps steps: W is read
+// once per row block, straight to registers in the MFMA layout; the X rows of
+// the range are staged in LDS with whole 128-byte row steps per load (X lives
+// in L2 and is read once per 64 latents).  Wave (g, sl) scores latent group g
+// (32 latents) over the range's steps sl and sl + 4; the four step lanes'
+// sums are added in a fixed order through LDS and written as whole rows.
 // ---------------------------------------------------------------------------
-constexpr int kSampleStride = 36;   // floats per LDS-staged row: 32 latents + pad (16-byte aligned)
+constexpr int kSampleStride = 68;   // floats per LDS-staged row of sums: 64 latents + pad (16-byte aligned)
 
 size_t sample_lds_bytes(int NB)
 {
-    return (size_t)4 * 32 * NB * kSampleStride * 4;
+    const size_t BT = 32 * (size_t)NB;
+    const size_t x = (size_t)kSampleSteps * BT * kXRowStride;
+    const size_t r = (size_t)4 * BT * kSampleStride * 4;
+    return x > r ? x : r;
 }
 
 template <int DT, int NB>
@@ -246,90 +250,98 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a)
     constexpr int ES = Dt<DT>::esize;
     constexpr int DS = Dt<DT>::DS;
     constexpr int BT = 32 * NB;
-    constexpr int SW = kSampleWaves;
+    constexpr int kChunks = kSampleSteps * BT * 8 / kSampleThreads;   // 16-byte X chunks per thread
     extern __shared__ __align__(16) unsigned char smem[];
-    float* T = (float*)smem;   // [4][BT][kSampleStride]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, jl = lane & 31;
-    const int nlb = a.nsamp / 32;
+    const int g = wave >> 2, sl = wave & 3;
+    const int nlb = a.nsamp / kSampleLat;
     const int lb = (int)(blockIdx.x % nlb);
     const int sp = (int)(blockIdx.x / nlb);
-    const int64_t ib = (int64_t)lb * 32;
+    const int64_t ib = (int64_t)lb * kSampleLat;
     const int64_t b0 = (int64_t)blockIdx.y * BT;
     const int64_t d = a.d;
     const int64_t nds = d / DS;   // d is a whole number of steps (checked on the host)
-    const int64_t sb = sp * nds / a.nsplit, se = (sp + 1) * nds / a.nsplit;
+    const int64_t sb = sp * nds / a.nsplit;
+    const int ns = (int)((sp + 1) * nds / a.nsplit - sb);   // 1 .. kSampleSteps (host)
 
-    const unsigned char* wp = (const unsigned char*)a.W + sample_latent(ib + jl, a.samp_log2) * d * ES + h * 64;
-    const unsigned char* xp[NB];
+    // X: chunk c is 16 bytes of row (c / 8) % BT at step c / (8 * BT); rows
+    // past B and steps past the range are staged as zeros.  The X loads go
+    // out first and W's after them, so waiting for X (in order) leaves the W
+    // loads in flight until the MFMAs.
+    const unsigned char* wp =
+        (const unsigned char*)a.W + (sample_latent(ib + 32 * g + jl, a.samp_log2) * d + sb * DS) * ES + h * 64;
+    u32x4 w[2][4];
+    {
+        u32x4 xr[kChunks];
+        uint32_t okm = 0;
 #pragma unroll
-    for (int n = 0; n < NB; ++n) {
-        // rows past B read row 0; their sums are never stored
-        const int64_t j = b0 + 32 * n + jl;
-        xp[n] = (const unsigned char*)a.X + (j < a.B ? j : 0) * d * ES + h * 64;
+        for (int p = 0; p < kChunks; ++p) {
+            // every load is in bounds (clamped row and step); a select at the
+            // store keeps branches, and the register copies they cause, out
+            const int c = tid + kSampleThreads * p;
+            const int c16 = c & 7, row = (c >> 3) % BT, st = (c >> 3) / BT;
+            const int64_t j = b0 + row;
+            okm |= (j < a.B && st < ns) ? (1u << p) : 0u;
+            const int64_t jc = j < a.B ? j : a.B - 1;
+            const int stc = st < ns ? st : ns - 1;
+            xr[p] = *(const u32x4*)((const unsigned char*)a.X + (jc * d + (sb + stc) * DS) * ES + c16 * 16);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // W of steps sl and sl + 4 (a step past the range reloads step 0; its X is zero)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int st = sl + 4 * t < ns ? sl + 4 * t : 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) w[t][q] = *(const u32x4*)(wp + st * kStepBytes + q * 16);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int p = 0; p < kChunks; ++p) {
+            const int c = tid + kSampleThreads * p;
+            const int c16 = c & 7, row = (c >> 3) % BT, st = (c >> 3) / BT;
+            *(u32x4*)(smem + (st * BT + row) * kXRowStride + c16 * 16) =
+                (okm >> p & 1u) ? xr[p] : u32x4{0u, 0u, 0u, 0u};
+        }
     }
+    __syncthreads();
 
     f32x16 acc[NB];
 #pragma unroll
     for (int n = 0; n < NB; ++n)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[n][r] = 0.f;
-    for (int64_t s0 = sb + wave; s0 < se; s0 += 2 * SW) {
-        u32x4 wq[2][4], xq[2][NB][4];
+    // steps past the range multiply the zeros staged for them (no branch
+    // around the MFMAs, whose accumulators would be copied at the join)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int64_t s = s0 + t * SW;
-            const int64_t sc = s < se ? s : s0;   // in bounds; its W is zeroed below
+    for (int t = 0; t < 2; ++t) {
+        const int st = sl + 4 * t;
+#pragma unroll
+        for (int n = 0; n < NB; ++n)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                wq[t][q] = *(const u32x4*)(wp + sc * kStepBytes + q * 16);
-#pragma unroll
-                for (int n = 0; n < NB; ++n) xq[t][n][q] = *(const u32x4*)(xp[n] + sc * kStepBytes + q * 16);
+                const u32x4 bx = *(const u32x4*)(smem + (st * BT + 32 * n + jl) * kXRowStride + h * 64 + q * 16);
+                mfma_quad<DT>(acc[n], w[t][q], bx);
             }
-            if (s >= se) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) wq[t][q] = u32x4{0u, 0u, 0u, 0u};
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int n = 0; n < NB; ++n) mfma_quad<DT>(acc[n], wq[t][q], xq[t][n][q]);
     }
+    __syncthreads();   // the X area becomes the staging area of the sums
 
-    // registers 4g..4g+3 of a lane hold latents 8g + 4h + 0..3 of row 32n + jl
-    auto stage = [&](float* buf) {
+    // registers 4e..4e+3 of a lane hold latents 32g + 8e + 4h + 0..3 of row 32n + jl
+    float* T = (float*)smem;   // [sl][BT][kSampleStride]
 #pragma unroll
-        for (int n = 0; n < NB; ++n)
+    for (int n = 0; n < NB; ++n)
 #pragma unroll
-            for (int g = 0; g < 4; ++g)
-                *(f32x4*)(buf + (32 * n + jl) * kSampleStride + 8 * g + 4 * h) =
-                    f32x4{acc[n][4 * g], acc[n][4 * g + 1], acc[n][4 * g + 2], acc[n][4 * g + 3]};
-    };
-    if (wave >= 4) stage(T + (wave - 4) * BT * kSampleStride);
-    __syncthreads();
-    if (wave < 4) {
-        float* buf = T + wave * BT * kSampleStride;
-#pragma unroll
-        for (int n = 0; n < NB; ++n)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const f32x4 v = *(const f32x4*)(buf + (32 * n + jl) * kSampleStride + 8 * g + 4 * h);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc[n][4 * g + e] += v[e];
-            }
-        stage(buf);
-    }
+        for (int e = 0; e < 4; ++e)
+            *(f32x4*)(T + (sl * BT + 32 * n + jl) * kSampleStride + 32 * g + 8 * e + 4 * h) =
+                f32x4{acc[n][4 * e], acc[n][4 * e + 1], acc[n][4 * e + 2], acc[n][4 * e + 3]};
     __syncthreads();
     float* Ps = a.P + (int64_t)sp * a.B * a.nsamp;
-    for (int c = tid; c < BT * 8; c += kSampleThreads) {
-        const int row = c >> 3, c4 = (c & 7) * 4;
+    constexpr int WS = BT * kSampleStride;
+    for (int c = tid; c < BT * 16; c += kSampleThreads) {
+        const int row = c >> 4, c4 = (c & 15) * 4;
         const int64_t j = b0 + row;
         if (j < a.B) {
             const float* t0 = T + row * kSampleStride + c4;
-            constexpr int WS = BT * kSampleStride;
             const f32x4 v = ((*(const f32x4*)t0 + *(const f32x4*)(t0 + WS)) + *(const f32x4*)(t0 + 2 * WS)) +
                             *(const f32x4*)(t0 + 3 * WS);
             *(f32x4*)(Ps + j * a.nsamp + ib + c4) = v;
@@ -355,24 +367,28 @@ __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
         if (tid == 0) { a.thr[row] = 0; a.list_cnt[row] = 0; }
         return;
     }
+    // item t of this thread is sampled latent 4 * tid + kThreads * 4 * (t / 4) + t % 4:
+    // four consecutive sampled latents (one 16-byte load of P) per quad
+    constexpr int kQuads = kItems / 4;
+    auto item = [&](int t) { return 4 * tid + kThreads * 4 * (t >> 2) + (t & 3); };
     const float* prow = a.P + row * (kItems * kThreads);
     const int64_t split_stride = (int64_t)gridDim.x * (kItems * kThreads);   // B rows per split
-    float v[kItems];
+    f32x4 v[kQuads];
 #pragma unroll
-    for (int t = 0; t < kItems; ++t) v[t] = prow[tid + t * kThreads];
+    for (int u = 0; u < kQuads; ++u) v[u] = *(const f32x4*)(prow + item(4 * u));
     for (int sp = 1; sp < a.nsplit; ++sp) {
 #pragma unroll
-        for (int t = 0; t < kItems; ++t) v[t] += prow[sp * split_stride + tid + t * kThreads];
+        for (int u = 0; u < kQuads; ++u) v[u] += *(const f32x4*)(prow + sp * split_stride + item(4 * u));
     }
-    if (a.bias != nullptr) {
+    if (a.bias != nullptr) {   // only 4-byte aligned: scalar loads
 #pragma unroll
-        for (int t = 0; t < kItems; ++t) v[t] += a.bias[sample_latent(tid + t * kThreads, a.samp_log2)];
+        for (int t = 0; t < kItems; ++t) v[t >> 2][t & 3] += a.bias[sample_latent(item(t), a.samp_log2)];
     }
     uint64_t key[kItems];
     uint64_t m = 0;
 #pragma unroll
     for (int t = 0; t < kItems; ++t) {
-        key[t] = make_key(v[t], sample_latent(tid + t * kThreads, a.samp_log2));
+        key[t] = make_key(v[t >> 2][t & 3], sample_latent(item(t), a.samp_log2));
         m = key[t] > m ? key[t] : m;
     }
     if (tid == 0) { S.cnt = 0; S.sel_cnt = 0; }
