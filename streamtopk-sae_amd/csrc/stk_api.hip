@@ -330,6 +330,7 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         if (e != hipSuccess) return hip_fail(e, "mainl_kernel launch");
         mg.list_keys = list_keys; mg.list_cnt = list_cnt; mg.list_cap = p.list_cap;
         mg.head_span = p.head_span; mg.nseg = p.nwg; mg.seg_cap = p.cap; mg.seg_cnt = ml.seg_cnt;
+        mg.spec = 0;
     } else {
         MainArgs ma;
         ma.X = X; ma.W = W; ma.bias = b; ma.B = B; ma.d = d; ma.F = F;
@@ -346,6 +347,9 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         if (e != hipSuccess) return hip_fail(e, "main_kernel launch");
         mg.list_keys = list_keys; mg.list_cnt = list_cnt; mg.list_cap = p.list_cap;
         mg.head_span = p.list_cap; mg.nseg = 0; mg.seg_cap = 1; mg.seg_cnt = nullptr;
+        // a sampled row keeps about k + k * F / nsamp candidates (the scores
+        // at or above the sample's k-th)
+        mg.spec = (p.sample && k + k * F / p.nsamp > 4096) ? 1 : 0;
     }
     mg.k = (int)k;
     mg.V = V; mg.I = I;

@@ -133,6 +133,8 @@ struct MergeArgs {
     int nseg, seg_cap;
     const int32_t* seg_cnt;      // [B][nseg]
     int k;
+    int spec;                    // non-zero: a dense list expected to hold more than
+                                 //   4096 candidates (one-chunk variant)
     float* V;
     int32_t* I;
 };

@@ -446,9 +446,14 @@ __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
 // fixed-size segments), read in chunks of kPer slots per thread.  Each chunk
 // is filtered against the larger of its own k-th of the per-thread maxima and
 // the k-th key of the last compaction.
+// kPer: candidate slots per thread and chunk.  kSpec > 0 (dense lists
+// expected to fill a whole chunk): the first kSpec slots per thread are loaded
+// at once, unconditionally (clamped into the row's list, masked afterwards),
+// together with the row's count; every other slot is loaded only if it holds
+// a candidate.
+template <int kPer, int kSpec>
 __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
 {
-    constexpr int kPer = 16;
     __shared__ SelShared S;
     __shared__ int scnt[kMergeMaxSeg];
     const int tid = threadIdx.x;
@@ -457,13 +462,18 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
     const int nseg = a.nseg;
     const int64_t hc = a.list_cnt[row];
     const uint64_t* keys = a.list_keys + row * a.list_cap;
+    uint64_t v[kPer];
+#pragma unroll
+    for (int u = 0; u < kSpec; ++u) {
+        const int64_t i = tid + (int64_t)u * kThreads;
+        v[u] = keys[i < a.list_cap ? i : a.list_cap - 1];
+    }
     for (int sg = tid; sg < nseg; sg += kThreads) scnt[sg] = a.seg_cnt[row * nseg + sg];
     const int64_t n = nseg ? a.head_span + (int64_t)nseg * a.seg_cap : hc;
     if (tid == 0) S.cnt = 0;
     __syncthreads();
     uint64_t run = 0;
     for (int64_t c0 = 0; c0 < n; c0 += (int64_t)kPer * kThreads) {
-        uint64_t v[kPer];
         uint64_t m = 0;
 #pragma unroll
         for (int u = 0; u < kPer; ++u) {
@@ -476,7 +486,10 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
             } else if (ok) {
                 ok = i < hc;
             }
-            v[u] = ok ? keys[i] : 0ull;
+            if (u < kSpec && c0 == 0)
+                v[u] = ok ? v[u] : 0ull;
+            else
+                v[u] = ok ? keys[i] : 0ull;
         }
 #pragma unroll
         for (int u = 0; u < kPer; ++u) m = v[u] > m ? v[u] : m;
@@ -581,7 +594,14 @@ hipError_t launch_thr(const ThrArgs& a, int64_t rows, hipStream_t st)
 
 hipError_t launch_merge(const MergeArgs& a, int64_t rows, hipStream_t st)
 {
-    launch(merge_kernel, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+    // dense lists expected to exceed one 4096-slot chunk: 32 slots per thread
+    // (one chunk), the first 16 loaded ahead of the count; otherwise 16 slots
+    // per thread, which also keeps the registers low enough for four
+    // workgroups per CU when the rows are many (large batches)
+    if (a.spec > 0)
+        launch(merge_kernel<32, 16>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+    else
+        launch(merge_kernel<16, 0>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     return hipGetLastError();
 }
 
