@@ -229,10 +229,10 @@ struct MainLoop {
 //
 // run() calls epi(t, acc, bias) after the last d-step of tile t (0-based
 // within the workgroup's tiles) and then clears acc.  The epilogue may use LDS
-// other than the X buffers and must neither issue global loads nor spill
-// registers (a scratch reload, like a global load, waits for every older
-// prefetched W load); the bias of tile t it receives was loaded during the
-// previous tile.
+// other than the X buffers and the bias buffers and must neither issue global
+// loads nor spill registers (a scratch reload, like a global load, waits for
+// every older prefetched W load); the bias of tile t it receives comes from
+// LDS, stored there during the previous tile.
 // ---------------------------------------------------------------------------
 template <int DT, int NB, int FRAGS, int WAVES>
 struct TileStream {
@@ -333,23 +333,45 @@ struct TileStream {
         }
     }
 
-    // Bias of this lane's latents of tile t: entry [a][r] is latent
-    // tile*kTileF + wave*32*FRAGS + a*32 + 8*(r/4) + 4*h + r%4 (0 past F).
-    __device__ __forceinline__ void tile_bias(float (&bv)[FRAGS][16], int t) const
+    // The bias goes through LDS (bias_lds: two kTileF-float buffers, by tile
+    // parity).  Wave 0 loads tile t+1's bias during tile t's d-steps and
+    // stores it to LDS within the same three-step iteration, so the compiler
+    // waits for those loads exactly (they are older than the step's own
+    // loads); the epilogue reads its bias from LDS and waits for no global
+    // load, so the prefetched W and X loads stay in flight across it.
+    __device__ __forceinline__ void bias_load(float (&bn)[kTileF / 64], int t) const
     {
-        const int64_t fw0 = (tile_begin + t) * kTileF + wave * (32 * FRAGS);
+        const int64_t f0 = (tile_begin + t) * kTileF + lane * (kTileF / 64);
+#pragma unroll
+        for (int e = 0; e < kTileF / 64; ++e) {
+            const int64_t f = f0 + e;
+            bn[e] = bias[(f < F) ? f : F - 1];
+        }
+    }
+
+    __device__ __forceinline__ void bias_store(const float (&bn)[kTileF / 64], float* buf) const
+    {
+#pragma unroll
+        for (int e = 0; e < kTileF / 64; ++e) buf[lane * (kTileF / 64) + e] = bn[e];
+    }
+
+    // Bias of this lane's latents: entry [a][r] is latent (within the tile)
+    // wave*32*FRAGS + a*32 + 8*(r/4) + 4*h + r%4.
+    __device__ __forceinline__ void bias_read(float (&bv)[FRAGS][16], const float* buf) const
+    {
 #pragma unroll
         for (int a = 0; a < FRAGS; ++a)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t f = fw0 + a * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-                bv[a][r] = bias[(f < F) ? f : F - 1];
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 v = *(const f32x4*)(buf + wave * (32 * FRAGS) + a * 32 + g * 8 + h * 4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) bv[a][4 * g + e] = v[e];
             }
     }
 
     template <class Epi>
     __device__ __forceinline__ void run(f32x16 (&acc)[FRAGS][NB], unsigned char* xs0, unsigned char* xs1,
-                                        unsigned char* xs2, Epi epi)
+                                        unsigned char* xs2, float* bias_lds, Epi epi)
     {
         if (ntiles <= 0) return;
         lt = 0;
@@ -357,8 +379,11 @@ struct TileStream {
         set_rows(0);
         u32x4 w0[FRAGS][4], w1[FRAGS][4], w2[FRAGS][4];
         u32x4 x0[kXChunks], x1[kXChunks], x2[kXChunks];
-        float bv[FRAGS][16];
-        tile_bias(bv, 0);
+        if (wave == 0) {
+            float bn[kTileF / 64];
+            bias_load(bn, 0);
+            bias_store(bn, bias_lds);
+        }
         issue(x0, w0);
         issue(x1, w1);
         issue(x2, w2);
@@ -371,7 +396,10 @@ struct TileStream {
                 for (int r = 0; r < 16; ++r) acc[a][n][r] = 0.f;
         __syncthreads();
         for (int t = 0; t < ntiles; ++t) {
+            float* bnext = bias_lds + ((t + 1) & 1) * kTileF;
             for (int s = 0; s < nds3; s += 3) {
+                float bn[kTileF / 64];
+                if (wave == 0) bias_load(bn, t + 1);   // past the last tile: clamped, unused
                 store_x(x1, xs1);
                 if (s < nds) compute(acc, w0, xs0);
                 issue(x0, w0);
@@ -383,10 +411,12 @@ struct TileStream {
                 store_x(x0, xs0);
                 if (s + 2 < nds) compute(acc, w2, xs2);
                 issue(x2, w2);
+                if (wave == 0) bias_store(bn, bnext);
                 __syncthreads();
             }
+            float bv[FRAGS][16];
+            bias_read(bv, bias_lds + (t & 1) * kTileF);
             epi(t, acc, bv);
-            if (t + 1 < ntiles) tile_bias(bv, t + 1);
 #pragma unroll
             for (int a = 0; a < FRAGS; ++a)
 #pragma unroll

@@ -62,6 +62,7 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
     uint64_t* q = (uint64_t*)(smem + 3 * BT * kXRowStride);
     const int cap = a.cap;
     uint64_t* thr = q + (size_t)BT * cap;
+    float* bias_lds = (float*)(thr + BT + 32);   // two tiles' bias (after the packed counts)
     // queue fill counts, 16 bits per row: word jl holds rows 32n + jl at bits
     // 16n, so one 64-bit LDS atomic reserves a lane's slots in all its rows
     uint64_t* cnt64 = thr + BT;
@@ -99,7 +100,7 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
 
     constexpr int kRowsPerWave = BT / WAVES;   // queue rows this wave compacts (<= 64)
     f32x16 acc[FRAGS][NB];
-    ts.run(acc, xs0, xs1, xs2, [&](int t, f32x16 (&ac)[FRAGS][NB], const float (&bias_r)[FRAGS][16]) {
+    ts.run(acc, xs0, xs1, xs2, bias_lds, [&](int t, f32x16 (&ac)[FRAGS][NB], const float (&bias_r)[FRAGS][16]) {
         // latent of accumulator register r of this lane: fl + 8*(r/4) + r%4
         const int64_t tile0 = (ts.tile_begin + t) * (int64_t)kTileLatents;
         const int64_t fl = tile0 + wave * 32 + h * 4;
@@ -534,7 +535,7 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
 size_t main_lds_bytes(int NB, int cap)
 {
     const size_t BT = 32 * (size_t)NB;
-    return 3 * BT * kXRowStride + BT * (size_t)cap * 8 + BT * 8 + 32 * 8;
+    return 3 * BT * kXRowStride + BT * (size_t)cap * 8 + BT * 8 + 32 * 8 + 2 * kTileLatents * 4;
 }
 
 template <int DT, int NB>
