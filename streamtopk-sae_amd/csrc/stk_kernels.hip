@@ -1,7 +1,8 @@
 // stk_kernels.hip -- the exact streaming top-k encoder on gfx950.
 //
-//   sample_kernel  : fp32 scores of the sampled latents (blocks of 128
-//                    consecutive latents spread over F) for every row.
+//   sample_kernel  : fp32 partial sums (one per d range) of the scores of the
+//                    sampled latents (blocks of 128 consecutive latents spread
+//                    over F) for every row.
 //   thr_kernel     : per row, the k-th largest sampled key: a lower bound of
 //                    the row's k-th key; the sample's top k open the row's
 //                    candidate list.
