@@ -192,6 +192,20 @@ def main():
         step()
     torch.cuda.synchronize()
     breakdown = read_profile(("sample_kernel", "thr_kernel", "main_kernel", "merge_kernel"))
+    # a plain read stream over W's bytes, timed the same way: the measured
+    # read ceiling the streaming kernel is compared with
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    w_bytes_all = W.numel() * W.element_size()
+    for _ in range(3):
+        _lib.check(lib.stk_read_probe(ctypes.c_void_p(W.data_ptr()), w_bytes_all, ctypes.c_void_p(sink.data_ptr()),
+                                      ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    torch.cuda.synchronize()
+    _lib.check(lib.stk_profile_enable(1))
+    for _ in range(20):
+        _lib.check(lib.stk_read_probe(ctypes.c_void_p(W.data_ptr()), w_bytes_all, ctypes.c_void_p(sink.data_ptr()),
+                                      ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    torch.cuda.synchronize()
+    probe_us = read_profile(("read_probe",))["read_probe"]["avg_us"]
     _lib.check(lib.stk_profile_enable(0))
 
     ms_per_step = 1e3 * wall / args.steps
@@ -218,6 +232,11 @@ def main():
     roof["traffic"] = traffic_from_profile(kname, args.workload)
     roof["alg_bytes_per_launch"] = alg_main
     roof["avg_launch_us"] = round(main_us, 2)
+    # measured read ceiling: the W bytes through a plain coalesced read kernel
+    stream_gbs = w_bytes_all / (probe_us * 1e-6) / 1e9
+    roof["measured_read_stream_GBs"] = round(stream_gbs, 1)
+    if roof["bound"] == "hbm":
+        roof["frac_of_measured_stream"] = round(bw_main / stream_gbs, 4)
 
     out = {
         "metric": METRIC if args.workload == "c2_bf16" else f"rows/s, {wl['label']}",

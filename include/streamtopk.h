@@ -89,6 +89,13 @@ int stk_approx_forward(const void* X, const void* W, const float* b, float* V, i
 int stk_cpu_forward(const float* X, const float* W, const float* b, float* V, int32_t* I,
                     int64_t B, int64_t d, int64_t F, int64_t k, int num_threads);
 
+/* Plain HBM read stream (no counterpart in the reference; used by bench.py to
+ * report the streaming kernels' bandwidth as a fraction of a measured read
+ * stream): reads `bytes` (a multiple of 16) from the 16-byte aligned device
+ * buffer `buf` once, coalesced, and XORs a digest of it into *sink (a device
+ * uint32), asynchronously on `stream`.  Timed under the name "read_probe". */
+int stk_read_probe(const void* buf, size_t bytes, uint32_t* sink, void* stream);
+
 /* Per-kernel timing (no counterpart in the reference; used by bench.py).
  * While enabled, every device entry point called on this thread records the
  * start and end of the kernels it launches with a HIP event pair carried in
@@ -101,8 +108,8 @@ int stk_profile_enable(int on);
 
 /* Total milliseconds and number of launches recorded for `kernel`
  * ("sample_kernel", "thr_kernel", "main_kernel", "merge_kernel",
- * "group_kernel", "cand_kernel") since profiling was enabled.  Waits for the
- * recorded events to complete. */
+ * "group_kernel", "cand_kernel", "read_probe") since profiling was enabled.
+ * Waits for the recorded events to complete. */
 int stk_profile_read(const char* kernel, double* total_ms, int64_t* launches);
 
 #ifdef __cplusplus

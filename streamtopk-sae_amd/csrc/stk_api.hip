@@ -128,7 +128,7 @@ static int ilog2_floor(int64_t x) { int l = 0; while ((x >> (l + 1)) > 0) ++l; r
 // ---------------------------------------------------------------------------
 struct ExactPlan {
     bool large;                  // mainl_kernel (B >= kLargeMinB) instead of main_kernel
-    int NB, cap;
+    int NB, cap, lq;             // lq: main_kernel's LDS queue keys per row
     int64_t nbc, num_tiles, tpw;
     int nwg;                     // main_kernel: W ranges; mainl_kernel: nr (grid = nbc * nr)
     bool sample;
@@ -136,7 +136,7 @@ struct ExactPlan {
     int ksplit;                  // d ranges (splits) of the sample pass
     int snb;                     // sample_kernel: 32-row tiles per workgroup
     int64_t list_cap, head_span;
-    size_t off_thr, off_P, off_list, off_lcnt, off_seg, total;
+    size_t off_thr, off_P, off_list, off_lcnt, off_seg, off_queue, total;
 };
 
 static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int dtype, int ncu)
@@ -144,6 +144,7 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
     ExactPlan p;
     p.num_tiles = cdiv(F, kTileLatents);
     p.large = B >= kLargeMinB;
+    p.lq = 0;
     if (p.large) {
         // 256-row blocks; W ranges a multiple of 8 so each range's row blocks share an XCD
         p.NB = kLargeRows / 32;
@@ -157,11 +158,10 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
         p.nwg = (int)nr;
     } else {
         const int64_t bblocks = cdiv(B > 0 ? B : 1, 32);
-        const int64_t nb_max = (k > 64) ? 2 : 4;   // k=128 queues need the LDS of 64 rows
-        p.NB = (int)(bblocks < nb_max ? bblocks : nb_max);
+        p.NB = (int)(bblocks < 4 ? bblocks : 4);
         if (p.NB == 3) p.NB = 4;
-        p.cap = (int)(k + 32);
-        if (p.cap & 1) ++p.cap;
+        p.lq = main_lds_queue(p.NB, (int)k);
+        p.cap = (int)((k + p.lq + 1) & ~(int64_t)1);
         p.nbc = cdiv(B, 32 * p.NB);
         int64_t nwg = ncu / (p.nbc > 0 ? p.nbc : 1);
         if (nwg < 1) nwg = 1;
@@ -204,7 +204,8 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
         p.ksplit = (int)ks;
     }
     p.head_span = p.sample ? p.nsamp : 0;
-    p.list_cap = p.head_span + (int64_t)p.nwg * p.cap;
+    // main_kernel: a workgroup leaves up to cap segment keys and lq queue keys per row
+    p.list_cap = p.head_span + (int64_t)p.nwg * (p.large ? p.cap : p.cap + p.lq);
     size_t off = 0;
     p.off_thr = off;
     off = align256(off + (size_t)B * 8);
@@ -216,6 +217,8 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
     off = align256(off + (size_t)B * 4);
     p.off_seg = off;
     if (p.large) off = align256(off + (size_t)B * p.nwg * 4);
+    p.off_queue = off;   // main_kernel: each workgroup's row queues
+    if (!p.large) off = align256(off + (size_t)p.nbc * p.nwg * 32 * p.NB * p.cap * 8);
     p.total = off;
     return p;
 }
@@ -341,6 +344,8 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         ma.samp_log2 = p.samp_log2;
         ma.samp_blocks = p.nsamp / kSampleBlock;
         ma.list_keys = list_keys; ma.list_cnt = list_cnt; ma.list_cap = p.list_cap;
+        ma.queue = (uint64_t*)(ws + p.off_queue);
+        ma.lq = p.lq;
         int pm = prof_begin("main_kernel", st);
         e = launch_main(dt, p.NB, ma, dim3((unsigned)p.nwg, (unsigned)p.nbc), st);
         prof_end(pm, st);
@@ -498,6 +503,23 @@ int stk_approx_forward(const void* X, const void* W, const float* b, float* V, i
     e = launch_cand(ca, B, st);
     prof_end(pg, st);
     if (e != hipSuccess) return hip_fail(e, "cand_kernel launch");
+    return 0;
+}
+
+int stk_read_probe(const void* buf, size_t bytes, uint32_t* sink, void* stream)
+{
+    clear_error();
+    if (!buf || !sink) return set_error(STK_E_INVALID, "null pointer");
+    if (((uintptr_t)buf & 15) || (bytes & 15)) return set_error(STK_E_INVALID, "buf and bytes must be 16-byte aligned");
+    if (bytes == 0) return 0;
+    int ncu = 0;
+    int rc;
+    if ((rc = cu_count(&ncu))) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    const int pi = prof_begin("read_probe", st);
+    const hipError_t e = launch_read_probe(buf, (int64_t)(bytes / 16), sink, ncu, st);
+    prof_end(pi, st);
+    if (e != hipSuccess) return hip_fail(e, "read_probe launch");
     return 0;
 }
 

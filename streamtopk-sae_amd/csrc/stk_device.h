@@ -427,4 +427,304 @@ struct TileStream {
     }
 };
 
+// ---------------------------------------------------------------------------
+// Compacts the queue segments (in global memory) of this wave's rows that are
+// full to their top-k: rows wave*R .. wave*R + R - 1 (R <= 64), segment of
+// row r at qrow(r), cap keys; cnt and thr in LDS.  Segment keys are read
+// through L2 (agent-scope atomic loads): other waves' plain stores are
+// complete (fence + barrier before the call) but the reading CU's L1 may hold
+// lines of an earlier compaction.  scr: cap keys of LDS for this wave.
+// ---------------------------------------------------------------------------
+template <int R, class RowSeg>
+__device__ __forceinline__ void compact_full_rows(int* cnt, uint64_t* thr, uint64_t* scr, RowSeg qrow,
+                                                  int cap, int k, int wave, int lane)
+{
+    const int myrow = wave * R + (lane < R ? lane : 0);
+    uint64_t full = __ballot(lane < R && cnt[myrow] >= cap);
+    while (full) {
+        const int i = __builtin_ctzll(full);
+        full &= full - 1;
+        const int row = wave * R + i;
+        uint64_t* q = qrow(row);
+        uint64_t e[3];
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            const int idx = lane + 64 * m;
+            e[m] = (idx < cap) ? __hip_atomic_load(q + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+            if (idx < cap) scr[idx] = e[m];
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        int rk[3] = {0, 0, 0};
+        for (int ii = 0; ii < cap; ii += 2) {
+            const u64x2 v = *(const u64x2*)(scr + ii);
+#pragma unroll
+            for (int m = 0; m < 3; ++m) rk[m] += (int)(v[0] > e[m]) + (int)(v[1] > e[m]);
+        }
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            if (lane + 64 * m < cap && rk[m] < k) {
+                q[rk[m]] = e[m];
+                if (rk[m] == k - 1) thr[row] = e[m];
+            }
+        }
+        if (lane == 0) cnt[row] = k;
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+// Rank-compacts the n keys q[0..n) (k < n <= cap <= 192, distinct, written
+// by this wave or read back through L2) to their k largest, in q[0..k), and
+// returns the k-th largest.  One wave; scr is cap keys of LDS scratch.
+__device__ __forceinline__ uint64_t compact_row(uint64_t* q, int n, uint64_t* scr, int cap, int k, int lane)
+{
+    uint64_t e[3];
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+        const int idx = lane + 64 * m;
+        e[m] = (idx < n) ? __hip_atomic_load(q + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+        if (idx < cap) scr[idx] = e[m];
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    // ranks among the n keys (the zero padding up to n rounded to even ranks below every key)
+    int rk[3] = {0, 0, 0};
+    for (int ii = 0; ii < n; ii += 2) {
+        const u64x2 v = *(const u64x2*)(scr + ii);
+#pragma unroll
+        for (int m = 0; m < 3; ++m) rk[m] += (int)(v[0] > e[m]) + (int)(v[1] > e[m]);
+    }
+    uint64_t kth = 0;
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+        if (lane + 64 * m < n && rk[m] < k) {
+            q[rk[m]] = e[m];
+            if (rk[m] == k - 1) kth = e[m];
+        }
+    }
+    // exactly one lane holds the k-th key
+    const uint64_t hit = __ballot(kth != 0);
+    const int src = __builtin_ctzll(hit);
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)kth, src);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(kth >> 32), src);
+    __builtin_amdgcn_wave_barrier();
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// ---------------------------------------------------------------------------
+// TileStream2: the score main loop with both operands staged in LDS.  A tile
+// is 32*WAVES latents x 32*NB rows and takes nds2 d-steps: the nds real ones
+// rounded up to even (a padding step loads a valid step again and skips its
+// MFMAs).
+//   W: each d-step's kTileF rows x 128 bytes are read with whole-line
+//      nontemporal loads (W is read once: no cache allocation), eight lanes
+//      per row step, two steps ahead in registers, and stored to a two-buffer
+//      LDS ring; each wave then reads its 32 rows in the MFMA layout.  Loads
+//      straight into the MFMA layout touch 32 rows per instruction, 32 bytes
+//      of each line, and stream W at ~6 TB/s; whole-line nontemporal loads
+//      reach ~7 TB/s.
+//   X: the row block's 32*NB rows of the step, the same way with ordinary
+//      loads (every workgroup of the row block re-reads X from L2).
+// One barrier per d-step.  The loads of the next tile's first steps are in
+// flight across the epilogue.  Every load is unconditional (rows past F or B
+// and steps past the end are clamped to valid addresses; the scores they
+// produce are never selected).
+//
+// run() calls epi(t, acc, bias) after the last d-step of tile t and then
+// clears acc and waits for every outstanding memory operation: the epilogue
+// may issue a data-dependent number of global stores, which the compiler
+// cannot count, and the wait restores its exact counts for the d-step loop
+// (the prefetched loads it includes have had the whole epilogue to land).
+// The epilogue may use LDS other than the rings and the bias buffers.  The
+// bias of tile t comes from LDS: wave 0 loads the next tile's bias inside the
+// d-step loop and stores it within the same iteration.
+// ---------------------------------------------------------------------------
+template <int DT, int NB, int WAVES>
+struct TileStream2 {
+    static constexpr int DS = Dt<DT>::DS;
+    static constexpr int ES = Dt<DT>::esize;
+    static constexpr int kThr = 64 * WAVES;
+    static constexpr int kTileF = 32 * WAVES;                      // latents per tile
+    static constexpr int kWChunks = kTileF * 8 / kThr;             // 16-byte W chunks per thread per step
+    static constexpr int kXTotal = 32 * NB * 8;                    // 16-byte X chunks per step
+    static constexpr int kXChunks = (kXTotal + kThr - 1) / kThr;   // per thread
+    static constexpr int kWBuf = kTileF * kXRowStride;             // bytes of one W ring buffer
+    static constexpr int kXBuf = 32 * NB * kXRowStride;            // bytes of one X ring buffer
+    static constexpr int kRingBytes = 2 * kWBuf + 2 * kXBuf;
+    static_assert(kXTotal % kThr == 0 || kXChunks == 1, "X chunk split");
+    static_assert(kTileF * 8 % kThr == 0, "W chunk split");
+
+    const float* bias;
+    int64_t F;
+    int64_t tile_begin;
+    int ntiles, nds, nds2;
+    int tid, lane, wave, h, jl;
+    const unsigned char* W;
+    int64_t w_row_bytes;
+
+    // load cursor (uniform) and this thread's chunk pointers in the cursor's tile
+    int lt, ls;
+    const unsigned char* lw[kWChunks];
+    const unsigned char* lx[kXChunks];
+    bool xok[kXChunks];
+
+    __device__ __forceinline__ void init_x(const unsigned char* X, int64_t B, int64_t b0, int64_t d)
+    {
+#pragma unroll
+        for (int p = 0; p < kXChunks; ++p) {
+            const int c = tid + kThr * p;
+            const int row = (c >> 3) % (32 * NB), c16 = c & 7;
+            int64_t r = b0 + row;
+            r = (r < B) ? r : B - 1;
+            lx[p] = X + (r * d) * ES + c16 * 16;
+            xok[p] = c < kXTotal;
+        }
+    }
+
+    __device__ __forceinline__ void set_rows(int t)
+    {
+        const int64_t tile = tile_begin + (t < ntiles ? t : ntiles - 1);
+#pragma unroll
+        for (int p = 0; p < kWChunks; ++p) {
+            const int c = tid + kThr * p;
+            int64_t f = tile * kTileF + (c >> 3);
+            f = (f < F) ? f : F - 1;
+            lw[p] = W + f * w_row_bytes + (c & 7) * 16;
+        }
+    }
+
+    __device__ __forceinline__ void issue(u32x4 (&xr)[kXChunks], u32x4 (&wr)[kWChunks])
+    {
+        const int s = (lt >= ntiles || ls >= nds) ? nds - 1 : ls;
+        const int64_t so = (int64_t)s * kStepBytes;
+#pragma unroll
+        for (int p = 0; p < kXChunks; ++p) xr[p] = *(const u32x4*)(lx[p] + so);
+#pragma unroll
+        for (int p = 0; p < kWChunks; ++p) wr[p] = __builtin_nontemporal_load((const u32x4*)(lw[p] + so));
+        if (lt < ntiles && ++ls == nds2) {
+            ls = 0;
+            ++lt;
+            if (lt < ntiles) set_rows(lt);
+        }
+    }
+
+    __device__ __forceinline__ void store(const u32x4 (&xr)[kXChunks], const u32x4 (&wr)[kWChunks],
+                                          unsigned char* xs, unsigned char* wsb) const
+    {
+#pragma unroll
+        for (int p = 0; p < kWChunks; ++p) {
+            const int c = tid + kThr * p;
+            *(u32x4*)(wsb + (c >> 3) * kXRowStride + (c & 7) * 16) = wr[p];
+        }
+#pragma unroll
+        for (int p = 0; p < kXChunks; ++p) {
+            const int c = tid + kThr * p;
+            if (kXTotal % kThr == 0 || xok[p]) *(u32x4*)(xs + (c >> 3) * kXRowStride + (c & 7) * 16) = xr[p];
+        }
+    }
+
+    __device__ __forceinline__ void compute(f32x16 (&acc)[NB], const unsigned char* xs, const unsigned char* wsb) const
+    {
+        u32x4 w[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) w[q] = *(const u32x4*)(wsb + (wave * 32 + jl) * kXRowStride + h * 64 + q * 16);
+        // two 32-row blocks at a time: two independent accumulation chains
+        constexpr int NP = NB < 2 ? NB : 2;
+#pragma unroll
+        for (int n0 = 0; n0 < NB; n0 += NP) {
+            u32x4 bx[NP][4];
+#pragma unroll
+            for (int n = 0; n < NP; ++n)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    bx[n][q] = *(const u32x4*)(xs + (32 * (n0 + n) + jl) * kXRowStride + h * 64 + q * 16);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int n = 0; n < NP; ++n) mfma_quad<DT>(acc[n0 + n], w[q], bx[n][q]);
+        }
+    }
+
+    __device__ __forceinline__ void bias_load(float (&bn)[kTileF / 64], int t) const
+    {
+        const int64_t f0 = (tile_begin + t) * kTileF + lane * (kTileF / 64);
+#pragma unroll
+        for (int e = 0; e < kTileF / 64; ++e) {
+            const int64_t f = f0 + e;
+            bn[e] = bias[(f < F) ? f : F - 1];
+        }
+    }
+
+    __device__ __forceinline__ void bias_store(const float (&bn)[kTileF / 64], float* buf) const
+    {
+#pragma unroll
+        for (int e = 0; e < kTileF / 64; ++e) buf[lane * (kTileF / 64) + e] = bn[e];
+    }
+
+    // Bias of this lane's latents: entry r is latent (within the tile)
+    // wave*32 + 8*(r/4) + 4*h + r%4.
+    __device__ __forceinline__ void bias_read(float (&bv)[16], const float* buf) const
+    {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const f32x4 v = *(const f32x4*)(buf + wave * 32 + g * 8 + h * 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bv[4 * g + e] = v[e];
+        }
+    }
+
+    template <class Epi>
+    __device__ __forceinline__ void run(f32x16 (&acc)[NB], unsigned char* ring, float* bias_lds, Epi epi)
+    {
+        if (ntiles <= 0) return;
+        unsigned char* ws0 = ring;
+        unsigned char* ws1 = ring + kWBuf;
+        unsigned char* xs0 = ring + 2 * kWBuf;
+        unsigned char* xs1 = ring + 2 * kWBuf + kXBuf;
+        lt = 0;
+        ls = 0;
+        set_rows(0);
+        u32x4 w0[kWChunks], w1[kWChunks];
+        u32x4 x0[kXChunks], x1[kXChunks];
+        if (wave == 0) {
+            float bn[kTileF / 64];
+            bias_load(bn, 0);
+            bias_store(bn, bias_lds);
+        }
+        issue(x0, w0);
+        issue(x1, w1);
+        store(x0, w0, xs0, ws0);
+        issue(x0, w0);
+#pragma unroll
+        for (int n = 0; n < NB; ++n)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[n][r] = 0.f;
+        __syncthreads();
+        for (int t = 0; t < ntiles; ++t) {
+            float* bnext = bias_lds + ((t + 1) & 1) * kTileF;
+            for (int s = 0; s < nds2; s += 2) {
+                float bn[kTileF / 64];
+                if (wave == 0) bias_load(bn, t + 1);   // past the last tile: clamped, unused
+                if (s < nds) compute(acc, xs0, ws0);
+                store(x1, w1, xs1, ws1);
+                issue(x1, w1);
+                __syncthreads();
+                if (s + 1 < nds) compute(acc, xs1, ws1);
+                store(x0, w0, xs0, ws0);
+                issue(x0, w0);
+                if (wave == 0) bias_store(bn, bnext);
+                __syncthreads();
+            }
+            float bv[16];
+            bias_read(bv, bias_lds + (t & 1) * kTileF);
+            epi(t, acc, bv);
+#pragma unroll
+            for (int n = 0; n < NB; ++n)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[n][r] = 0.f;
+            __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+        }
+    }
+};
+
 }  // namespace stk

@@ -65,8 +65,10 @@ struct MainArgs {
     int samp_log2, samp_blocks;  //   scored by the sample pass and are skipped here
     uint64_t* list_keys;         // [B][list_cap]: every workgroup's final queue, appended
     int32_t* list_cnt;           // [B] keys in each row's list (set by thr_kernel)
-    int64_t list_cap;            // nsamp + nwg * cap: room for the sampled keys
-                                 //   and every workgroup's full queue
+    int64_t list_cap;            // nsamp + nwg * (cap + lq): room for the sampled
+                                 //   keys and every workgroup's keys
+    uint64_t* queue;             // [nbc][nwg][32*NB][cap] each workgroup's row segments
+    int lq;                      // LDS queue keys per row (even, <= 64; cap >= k + lq)
 };
 
 constexpr int kSampleWaves = 8;      // wavefronts per sample_kernel workgroup
@@ -159,7 +161,8 @@ struct CandArgs {                // approximate variant, top-k over the candidat
     int32_t* I;
 };
 
-size_t main_lds_bytes(int NB, int cap);
+size_t main_lds_bytes(int NB, int cap, int lq);
+int main_lds_queue(int NB, int k);
 size_t mainl_lds_bytes(int cap);
 size_t group_lds_bytes(int NB);
 
@@ -171,5 +174,6 @@ hipError_t launch_thr(const ThrArgs& a, int64_t rows, hipStream_t st);
 hipError_t launch_merge(const MergeArgs& a, int64_t rows, hipStream_t st);
 hipError_t launch_group(int dt, int NB, const GroupArgs& a, dim3 grid, hipStream_t st);
 hipError_t launch_cand(const CandArgs& a, int64_t rows, hipStream_t st);
+hipError_t launch_read_probe(const void* buf, int64_t n16, uint32_t* sink, int ncu, hipStream_t st);
 
 }  // namespace stk

@@ -9,10 +9,10 @@
 //   main_kernel    : streams W once; MFMA scores for 256 latents x up to 128
 //                    rows per tile (the sampled latents are skipped: each latent
 //                    is scored by exactly one kernel); scores not below the
-//                    row threshold go to a
-//                    per-row LDS queue that is rank-compacted to its top-k
-//                    whenever it fills.  Appends each workgroup's final queue to
-//                    a dense per-row candidate list.
+//                    row threshold go to a short per-row LDS queue, which
+//                    spills to a per-row global segment when it fills; a full
+//                    segment is rank-compacted to its top-k.  Appends each
+//                    workgroup's keys to a dense per-row candidate list.
 //   merge_kernel   : per row, top-k of its candidate list.
 //
 // The reference's pass 1 / pass 2 split (streamtopk_exact.cu:58-187 tile
@@ -49,38 +49,77 @@ __device__ __forceinline__ float pick16(const f32x16& v, uint32_t r)
 // ---------------------------------------------------------------------------
 // main_kernel
 // ---------------------------------------------------------------------------
+// Spills the full LDS queues among this wave's rows (wave*R .. wave*R+R-1)
+// to their global segments: a segment without room for a whole LDS queue is
+// first rank-compacted to its top k (raising the row threshold), then the
+// LDS keys above the threshold are appended.  Every global access of a row is
+// made by the wave that owns the row.  Ends with the wave's stores complete.
+template <int R>
+__device__ __forceinline__ void spill_full_rows(int* cnt, int* gcnt, uint64_t* thr, const uint64_t* lqk,
+                                                uint64_t* seg, uint64_t* scr, int lq, int cap, int k, int wave,
+                                                int lane)
+{
+    const int myrow = wave * R + (lane < R ? lane : 0);
+    uint64_t full = __ballot(lane < R && cnt[myrow] >= lq);
+    while (full) {
+        const int i = __builtin_ctzll(full);
+        full &= full - 1;
+        const int row = wave * R + i;
+        uint64_t* q = seg + (size_t)row * cap;
+        int g = gcnt[row];
+        uint64_t t = thr[row];
+        if (g + lq > cap) {
+            t = compact_row(q, g, scr, cap, k, lane);
+            g = k;
+        }
+        // lq <= 64: one key per lane
+        const uint64_t key = lane < lq ? lqk[row * lq + lane] : 0ull;
+        const bool f = key > t;
+        const uint64_t bal = __ballot(f);
+        const int pos = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                       __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+        if (f) q[g + pos] = key;
+        if (lane == 0) {
+            thr[row] = t;
+            gcnt[row] = g + __popcll(bal);
+            cnt[row] = 0;
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the segment stores are complete
+}
+
 template <int DT, int NB>
 __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
 {
     constexpr int BT = 32 * NB;
-    constexpr int FRAGS = 1;
     constexpr int WAVES = kMainWaves;
-    constexpr int DS = Dt<DT>::DS;
+    constexpr int R = BT / WAVES;   // rows each wave spills and flushes
+    using TS = TileStream2<DT, NB, WAVES>;
     extern __shared__ __align__(16) unsigned char smem[];
-    unsigned char* xs0 = smem;
-    unsigned char* xs1 = smem + BT * kXRowStride;
-    unsigned char* xs2 = smem + 2 * BT * kXRowStride;
-    uint64_t* q = (uint64_t*)(smem + 3 * BT * kXRowStride);
-    const int cap = a.cap;
-    uint64_t* thr = q + (size_t)BT * cap;
-    float* bias_lds = (float*)(thr + BT + 32);   // two tiles' bias (after the packed counts)
-    // queue fill counts, 16 bits per row: word jl holds rows 32n + jl at bits
-    // 16n, so one 64-bit LDS atomic reserves a lane's slots in all its rows
-    uint64_t* cnt64 = thr + BT;
-    uint16_t* cnt = (uint16_t*)cnt64;
-    auto ci = [](int row) { return 4 * (row & 31) + (row >> 5); };
+    const int cap = a.cap, lq = a.lq;
+    uint64_t* thr = (uint64_t*)(smem + TS::kRingBytes);          // [BT] row threshold keys
+    int* cnt = (int*)(thr + BT);                                   // [BT] LDS queue fill counts
+    int* gcnt = cnt + BT;                                          // [BT] global segment fill counts
+    float* bias_lds = (float*)(gcnt + BT);                         // [2][kTileLatents]
+    uint64_t* lqk = (uint64_t*)(bias_lds + 2 * kTileLatents);      // [BT][lq] LDS queues
+    uint64_t* cscr = lqk + BT * lq;                                // [WAVES][cap] compaction scratch
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, jl = lane & 31;
     const int64_t b0 = (int64_t)blockIdx.y * BT;
     const int64_t B = a.B, F = a.F;
     const int k = a.k;
+    // this workgroup's global segments: cap keys per row
+    uint64_t* seg = a.queue + ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * BT * cap;
 
-    for (int i = tid; i < BT; i += kMainThreads)
+    for (int i = tid; i < BT; i += kMainThreads) {
         thr[i] = (a.thr0 != nullptr && b0 + i < B) ? a.thr0[b0 + i] : 0ull;
-    if (tid < 32) cnt64[tid] = 0;
+        cnt[i] = 0;
+        gcnt[i] = 0;
+    }
 
-    TileStream<DT, NB, FRAGS, WAVES> ts;
+    TS ts;
     ts.W = (const unsigned char*)a.W;
     ts.w_row_bytes = a.d * Dt<DT>::esize;
     ts.bias = a.bias;
@@ -90,8 +129,8 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
         const int64_t t1 = ts.tile_begin + a.tiles_per_wg;
         ts.ntiles = (int)((t1 < a.num_tiles ? t1 : a.num_tiles) - ts.tile_begin);
     }
-    ts.nds = (int)(a.d / DS);
-    ts.nds3 = (ts.nds + 2) / 3 * 3;
+    ts.nds = (int)(a.d / Dt<DT>::DS);
+    ts.nds2 = (ts.nds + 1) / 2 * 2;
     ts.tid = tid;
     ts.lane = lane;
     ts.wave = wave;
@@ -99,9 +138,8 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
     ts.jl = jl;
     ts.init_x((const unsigned char*)a.X, B, b0, a.d);
 
-    constexpr int kRowsPerWave = BT / WAVES;   // queue rows this wave compacts (<= 64)
-    f32x16 acc[FRAGS][NB];
-    ts.run(acc, xs0, xs1, xs2, bias_lds, [&](int t, f32x16 (&ac)[FRAGS][NB], const float (&bias_r)[FRAGS][16]) {
+    f32x16 acc[NB];
+    ts.run(acc, smem, bias_lds, [&](int t, f32x16 (&ac)[NB], const float (&bias_r)[16]) {
         // latent of accumulator register r of this lane: fl + 8*(r/4) + r%4
         const int64_t tile0 = (ts.tile_begin + t) * (int64_t)kTileLatents;
         const int64_t fl = tile0 + wave * 32 + h * 4;
@@ -129,35 +167,32 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
             uint32_t m = 0;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                ac[0][n][r] += bias_r[0][r];
-                m |= (!(ac[0][n][r] < tv)) ? (1u << r) : 0u;
+                ac[n][r] += bias_r[r];
+                m |= (!(ac[n][r] < tv)) ? (1u << r) : 0u;
             }
             pend[n] = (b0 + j < B) ? (m & vmask) : 0u;
         }
 
-        // ---- append; compact full queues and retry while anything overflowed ----
+        // ---- append to the LDS queues; spill full ones and retry while anything overflowed ----
         for (int it = 0; it < 4096; ++it) {
             bool overflow = false;
             // reserve the slots of every row block first, then wait once
-            uint64_t add = 0;
-#pragma unroll
-            for (int n = 0; n < NB; ++n) add |= (uint64_t)__builtin_popcount(pend[n]) << (16 * n);
-            // a field never carries into the next: counts stay below cap + 512
-            const uint64_t old = add ? atomicAdd((unsigned long long*)&cnt64[jl], (unsigned long long)add) : 0ull;
             int base[NB];
 #pragma unroll
-            for (int n = 0; n < NB; ++n) base[n] = (int)((old >> (16 * n)) & 0xFFFFu);
+            for (int n = 0; n < NB; ++n)
+                base[n] = pend[n] ? atomicAdd(&cnt[32 * n + jl], __builtin_popcount(pend[n])) : 0;
+            __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
 #pragma unroll
             for (int n = 0; n < NB; ++n) {
-                // this lane's survivors only (about 1 in 50 scores), lowest register first
-                uint64_t* qj = q + (size_t)(32 * n + jl) * cap;
+                // this lane's survivors only (a few per cent of the scores), lowest register first
+                uint64_t* qj = lqk + (32 * n + jl) * lq;
                 uint32_t m = pend[n], keep = 0;
                 int slot = base[n];
                 while (m) {
                     const uint32_t r = (uint32_t)__builtin_ctz(m);
                     m &= m - 1u;
-                    if (slot < cap)
-                        qj[slot] = make_key(pick16(ac[0][n], r), fl + (r >> 2) * 8 + (r & 3));
+                    if (slot < lq)
+                        qj[slot] = make_key(pick16(ac[n], r), fl + (r >> 2) * 8 + (r & 3));
                     else
                         keep |= 1u << r;
                     ++slot;
@@ -166,34 +201,8 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
                 overflow |= keep != 0;
             }
             if (!__syncthreads_or(overflow)) break;
-            // wave w compacts its rows w*kRowsPerWave + i whose queue is full
-            {
-                const int myrow = wave * kRowsPerWave + (lane < kRowsPerWave ? lane : 0);
-                uint64_t full = __ballot(lane < kRowsPerWave && cnt[ci(myrow)] >= cap);
-                while (full) {
-                    const int i = __builtin_ctzll(full);
-                    full &= full - 1;
-                    const int row = wave * kRowsPerWave + i;
-                    uint64_t* qr = q + (size_t)row * cap;
-                    uint64_t e[3];
-                    int rk[3] = {0, 0, 0};
-#pragma unroll
-                    for (int mm = 0; mm < 3; ++mm) e[mm] = (lane + 64 * mm < cap) ? qr[lane + 64 * mm] : 0ull;
-                    for (int ii = 0; ii < cap; ii += 2) {
-                        const u64x2 v = *(const u64x2*)(qr + ii);
-#pragma unroll
-                        for (int mm = 0; mm < 3; ++mm) rk[mm] += (int)(v[0] > e[mm]) + (int)(v[1] > e[mm]);
-                    }
-#pragma unroll
-                    for (int mm = 0; mm < 3; ++mm) {
-                        if (lane + 64 * mm < cap && rk[mm] < k) {
-                            qr[rk[mm]] = e[mm];
-                            if (rk[mm] == k - 1) thr[row] = e[mm];
-                        }
-                    }
-                    if (lane == 0) cnt[ci(row)] = (uint16_t)k;
-                }
-            }
+            __syncthreads();   // the LDS queues are complete
+            spill_full_rows<R>(cnt, gcnt, thr, lqk, seg, cscr + wave * cap, lq, cap, k, wave, lane);
             __syncthreads();
             // drop pending scores that fell below a raised threshold
 #pragma unroll
@@ -203,25 +212,28 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
                 while (m) {
                     const uint32_t r = (uint32_t)__builtin_ctz(m);
                     m &= m - 1u;
-                    if (!(make_key(pick16(ac[0][n], r), fl + (r >> 2) * 8 + (r & 3)) > tk)) pend[n] &= ~(1u << r);
+                    if (!(make_key(pick16(ac[n], r), fl + (r >> 2) * 8 + (r & 3)) > tk)) pend[n] &= ~(1u << r);
                 }
             }
         }
     });
 
-    // ---- append this workgroup's queues to the rows' candidate lists ----
+    // ---- append this workgroup's keys to the rows' candidate lists: each
+    // wave its R rows, the global segment's keys then the LDS queue's ----
     __syncthreads();
-    int* lbase = (int*)thr;   // the thresholds are no longer needed
-    for (int i = tid; i < BT; i += kMainThreads) {
-        const int c = (b0 + i < B) ? (cnt[ci(i)] < cap ? cnt[ci(i)] : cap) : 0;
-        cnt[ci(i)] = (uint16_t)c;
-        lbase[i] = c ? atomicAdd(&a.list_cnt[b0 + i], c) : 0;
-    }
-    __syncthreads();
-    for (int idx = tid; idx < BT * cap; idx += kMainThreads) {
-        const int row = idx / cap, e = idx - row * cap;
-        if (e < cnt[ci(row)])
-            a.list_keys[(size_t)(b0 + row) * a.list_cap + lbase[row] + e] = q[(size_t)row * cap + e];
+    const int myrow = wave * R + (lane < R ? lane : 0);
+    const bool own = lane < R && b0 + myrow < B;
+    const int nl = own ? (cnt[myrow] < lq ? cnt[myrow] : lq) : 0;
+    const int ng = own ? gcnt[myrow] : 0;
+    const int lbase = (nl + ng) ? atomicAdd(&a.list_cnt[b0 + myrow], nl + ng) : 0;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int rl = __shfl(nl, i, 64), rg = __shfl(ng, i, 64), rb = __shfl(lbase, i, 64);
+        const int row = wave * R + i;
+        uint64_t* dst = a.list_keys + (size_t)(b0 + row) * a.list_cap + rb;
+        const uint64_t* q = seg + (size_t)row * cap;
+        for (int e = lane; e < rg; e += 64) dst[e] = __hip_atomic_load(q + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane < rl) dst[rg + lane] = lqk[row * lq + lane];
     }
 }
 
@@ -531,18 +543,61 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// read_probe_kernel: reads n16 16-byte words once and folds them (XOR) into
+// *sink with one atomic per wave, so that no load can be elided.  Each
+// workgroup streams one contiguous chunk, 64 KiB per round (eight coalesced
+// 8 KiB loads in flight per thread): a plain HBM read stream to compare the
+// streaming kernels with.
+// ---------------------------------------------------------------------------
+constexpr int kProbeThreads = 512;
+
+__global__ __launch_bounds__(kProbeThreads) void read_probe_kernel(const u32x4* p, int64_t n16, uint32_t* sink)
+{
+    const int64_t per = (n16 + gridDim.x - 1) / gridDim.x;
+    const int64_t lo = (int64_t)blockIdx.x * per;
+    const int64_t hi = lo + per < n16 ? lo + per : n16;
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    int64_t i = lo + threadIdx.x;
+    for (; i + 7 * kProbeThreads < hi; i += 8 * kProbeThreads) {
+        u32x4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = p[i + u * kProbeThreads];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc ^= v[u];
+    }
+    for (; i < hi; i += kProbeThreads) acc ^= p[i];
+    uint32_t x = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x ^= __shfl_xor(x, off, 64);
+    if ((threadIdx.x & 63) == 0) atomicXor(sink, x);
+}
+
+// ---------------------------------------------------------------------------
 // Host-side launch helpers
 // ---------------------------------------------------------------------------
-size_t main_lds_bytes(int NB, int cap)
+size_t main_lds_bytes(int NB, int cap, int lq)
 {
     const size_t BT = 32 * (size_t)NB;
-    return 3 * BT * kXRowStride + BT * (size_t)cap * 8 + BT * 8 + 32 * 8 + 2 * kTileLatents * 4;
+    const size_t rings = 2 * (size_t)kTileLatents * kXRowStride + 2 * BT * kXRowStride;   // TileStream2
+    return rings + BT * 8 + BT * 8 + 2 * kTileLatents * 4 + BT * (size_t)lq * 8 + (size_t)kMainWaves * cap * 8;
+}
+
+// LDS queue keys per row: the most (even, at most 64) whose LDS use, with
+// global segments of cap = k + lq keys, fits the workgroup's 160 KiB (less
+// 1 KiB for the kernel's static LDS: __syncthreads_or's reduction).
+int main_lds_queue(int NB, int k)
+{
+    for (int lq = 64; lq >= 2; lq -= 2) {
+        const int cap = (k + lq + 1) & ~1;
+        if (main_lds_bytes(NB, cap, lq) <= 159 * 1024) return lq;
+    }
+    return 0;
 }
 
 template <int DT, int NB>
 static hipError_t launch_main_t(const MainArgs& a, dim3 grid, hipStream_t st)
 {
-    const size_t lds = main_lds_bytes(NB, a.cap);
+    const size_t lds = main_lds_bytes(NB, a.cap, a.lq);
     auto kern = main_kernel<DT, NB>;
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
@@ -591,6 +646,12 @@ hipError_t launch_thr(const ThrArgs& a, int64_t rows, hipStream_t st)
     }
     if (a.P != nullptr && a.nsamp != kSampleTarget) return hipErrorInvalidValue;
     launch(thr_kernel<kSampleTarget / kThreads>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_read_probe(const void* buf, int64_t n16, uint32_t* sink, int ncu, hipStream_t st)
+{
+    launch(read_probe_kernel, dim3((unsigned)(2 * ncu)), dim3(kProbeThreads), 0, st, (const u32x4*)buf, n16, sink);
     return hipGetLastError();
 }
 

@@ -197,48 +197,6 @@ __device__ __forceinline__ float agpr_read(float x)
     return r;
 }
 
-// Compacts the segments of this wave's rows that are full to their top-k.
-// Segment keys are read through L2 (agent-scope atomic loads): other waves'
-// plain stores are complete (fence + barrier before the call) but the
-// reading CU's L1 may hold lines of an earlier compaction.
-__device__ __forceinline__ void compact_full_rows(int* cnt, uint64_t* thr, uint64_t* scr, uint64_t* const* qrow,
-                                                  int cap, int k, int wave, int lane)
-{
-    constexpr int kRowsPerWave = kLargeRows / kLWaves;   // 64
-    const int myrow = wave * kRowsPerWave + lane;
-    uint64_t full = __ballot(cnt[myrow] >= cap);
-    while (full) {
-        const int i = __builtin_ctzll(full);
-        full &= full - 1;
-        const int row = wave * kRowsPerWave + i;
-        uint64_t* q = qrow[row];
-        uint64_t e[3];
-#pragma unroll
-        for (int m = 0; m < 3; ++m) {
-            const int idx = lane + 64 * m;
-            e[m] = (idx < cap) ? __hip_atomic_load(q + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
-            if (idx < cap) scr[idx] = e[m];
-        }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        int rk[3] = {0, 0, 0};
-        for (int ii = 0; ii < cap; ii += 2) {
-            const u64x2 v = *(const u64x2*)(scr + ii);
-#pragma unroll
-            for (int m = 0; m < 3; ++m) rk[m] += (int)(v[0] > e[m]) + (int)(v[1] > e[m]);
-        }
-#pragma unroll
-        for (int m = 0; m < 3; ++m) {
-            if (lane + 64 * m < cap && rk[m] < k) {
-                q[rk[m]] = e[m];
-                if (rk[m] == k - 1) thr[row] = e[m];
-            }
-        }
-        if (lane == 0) cnt[row] = k;
-        __builtin_amdgcn_wave_barrier();
-    }
-}
-
 }  // namespace
 
 size_t mainl_lds_bytes(int cap)
@@ -477,7 +435,8 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                 if (!__syncthreads_or(overflow)) break;
                 __threadfence_block();   // this thread's segment stores are complete
                 __syncthreads();
-                compact_full_rows(cnt, thr, cscr + wave * cap, qrow, cap, k, wave, lane);
+                compact_full_rows<kLargeRows / kLWaves>(cnt, thr, cscr + wave * cap,
+                                                       [&](int r) { return qrow[r]; }, cap, k, wave, lane);
                 __threadfence_block();
                 __syncthreads();
 #pragma unroll

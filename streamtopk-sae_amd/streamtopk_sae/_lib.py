@@ -31,6 +31,7 @@ SIGNATURES = {
     "stk_approx_forward": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int,
                                   _vp, _vp, _vp, ctypes.c_size_t, _vp]),
     "stk_cpu_forward": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int]),
+    "stk_read_probe": (_int, [_vp, ctypes.c_size_t, _vp, _vp]),
     "stk_profile_enable": (_int, [_int]),
     "stk_profile_read": (_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                                 ctypes.POINTER(ctypes.c_int64)]),
