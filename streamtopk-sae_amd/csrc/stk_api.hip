@@ -214,7 +214,7 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
     p.off_list = off;
     off = align256(off + (size_t)B * p.list_cap * 8);
     p.off_lcnt = off;
-    off = align256(off + (size_t)B * 4);
+    off = align256(off + (size_t)B * 4 * kCntStride);
     p.off_seg = off;
     if (p.large) off = align256(off + (size_t)B * p.nwg * 4);
     p.off_queue = off;   // main_kernel: each workgroup's row queues

@@ -64,12 +64,17 @@ struct MainArgs {
     int sampled;                 // non-zero: the sampled latents (is_sampled) were
     int samp_log2, samp_blocks;  //   scored by the sample pass and are skipped here
     uint64_t* list_keys;         // [B][list_cap]: every workgroup's final queue, appended
-    int32_t* list_cnt;           // [B] keys in each row's list (set by thr_kernel)
+    int32_t* list_cnt;           // [B * kCntStride] keys in each row's list (set by thr_kernel)
     int64_t list_cap;            // nsamp + nwg * (cap + lq): room for the sampled
                                  //   keys and every workgroup's keys
     uint64_t* queue;             // [nbc][nwg][32*NB][cap] each workgroup's row segments
     int lq;                      // LDS queue keys per row (even, <= 64; cap >= k + lq)
 };
+
+// Row r's candidate count is list_cnt[r * kCntStride]: one 128-byte line per
+// row, so that the workgroups' end-of-kernel atomics on different rows do not
+// queue on the same L2 line.
+constexpr int kCntStride = 32;
 
 constexpr int kSampleWaves = 8;      // wavefronts per sample_kernel workgroup
 constexpr int kSampleThreads = 64 * kSampleWaves;
@@ -93,7 +98,7 @@ struct ThrArgs {
     int samp_log2, nsamp, k;
     uint64_t* thr;               // [B] row threshold keys
     uint64_t* list_keys;         // [B][list_cap]: receives the sampled keys >= thr
-    int32_t* list_cnt;           // [B] set to the number of those keys
+    int32_t* list_cnt;           // [B * kCntStride] set to the number of those keys
     int64_t list_cap;
 };
 
@@ -122,15 +127,15 @@ struct MainLArgs {
     float* P;                    // [ksplit][B][nsamp]
 };
 
-// A row's candidates: slots [0, head_span) hold list_cnt[row] keys at their
+// A row's candidates: slots [0, head_span) hold list_cnt[row * kCntStride] keys at their
 // front; then nseg segments of seg_cap slots, segment s holding
 // seg_cnt[row * nseg + s] keys at its front.  With nseg == 0 the row is the
-// dense list [0, list_cnt[row]).
+// dense list [0, list_cnt[row * kCntStride]).
 constexpr int kMergeMaxSeg = 1024;
 
 struct MergeArgs {
     const uint64_t* list_keys;   // [B][list_cap]
-    const int32_t* list_cnt;     // [B]
+    const int32_t* list_cnt;     // [B * kCntStride]
     int64_t list_cap, head_span;
     int nseg, seg_cap;
     const int32_t* seg_cnt;      // [B][nseg]

@@ -174,6 +174,12 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
         }
 
         // ---- append to the LDS queues; spill full ones and retry while anything overflowed ----
+        // The second ring buffers are idle during the epilogue: the W one holds
+        // each wave's scores of one row block as [r][lane] (a survivor's score
+        // is one LDS read away: a lane cannot index its own registers), the X
+        // one a slot per thread that absorbs the writes of overflowing survivors.
+        float* sc = (float*)(smem + TS::kWBuf) + wave * 16 * 64;
+        uint64_t* dump = (uint64_t*)(smem + 2 * TS::kWBuf + TS::kXBuf) + tid;
         for (int it = 0; it < 4096; ++it) {
             bool overflow = false;
             // reserve the slots of every row block first, then wait once
@@ -181,9 +187,10 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
 #pragma unroll
             for (int n = 0; n < NB; ++n)
                 base[n] = pend[n] ? atomicAdd(&cnt[32 * n + jl], __builtin_popcount(pend[n])) : 0;
-            __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
 #pragma unroll
             for (int n = 0; n < NB; ++n) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sc[r * 64 + lane] = ac[n][r];
                 // this lane's survivors only (a few per cent of the scores), lowest register first
                 uint64_t* qj = lqk + (32 * n + jl) * lq;
                 uint32_t m = pend[n], keep = 0;
@@ -191,10 +198,9 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
                 while (m) {
                     const uint32_t r = (uint32_t)__builtin_ctz(m);
                     m &= m - 1u;
-                    if (slot < lq)
-                        qj[slot] = make_key(pick16(ac[n], r), fl + (r >> 2) * 8 + (r & 3));
-                    else
-                        keep |= 1u << r;
+                    const bool ok = slot < lq;
+                    *(ok ? qj + slot : dump) = make_key(sc[r * 64 + lane], fl + (r >> 2) * 8 + (r & 3));
+                    keep |= ok ? 0u : (1u << r);
                     ++slot;
                 }
                 pend[n] = keep;
@@ -225,7 +231,7 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
     const bool own = lane < R && b0 + myrow < B;
     const int nl = own ? (cnt[myrow] < lq ? cnt[myrow] : lq) : 0;
     const int ng = own ? gcnt[myrow] : 0;
-    const int lbase = (nl + ng) ? atomicAdd(&a.list_cnt[b0 + myrow], nl + ng) : 0;
+    const int lbase = (nl + ng) ? atomicAdd(&a.list_cnt[(b0 + myrow) * kCntStride], nl + ng) : 0;
 #pragma unroll
     for (int i = 0; i < R; ++i) {
         const int rl = __shfl(nl, i, 64), rg = __shfl(ng, i, 64), rb = __shfl(lbase, i, 64);
@@ -378,7 +384,7 @@ __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
     if (a.P == nullptr) {
-        if (tid == 0) { a.thr[row] = 0; a.list_cnt[row] = 0; }
+        if (tid == 0) { a.thr[row] = 0; a.list_cnt[row * kCntStride] = 0; }
         return;
     }
     // item t of this thread is sampled latent 4 * tid + kThreads * 4 * (t / 4) + t % 4:
@@ -452,7 +458,7 @@ __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
     __syncthreads();
     if (tid == 0) {
         a.thr[row] = T;
-        a.list_cnt[row] = S.sel_cnt;
+        a.list_cnt[row * kCntStride] = S.sel_cnt;
     }
 }
 
@@ -474,7 +480,7 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
     const int64_t row = blockIdx.x;
     const int k = a.k;
     const int nseg = a.nseg;
-    const int64_t hc = a.list_cnt[row];
+    const int64_t hc = a.list_cnt[row * kCntStride];
     const uint64_t* keys = a.list_keys + row * a.list_cap;
     uint64_t v[kPer];
 #pragma unroll
@@ -546,8 +552,9 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
 // read_probe_kernel: reads n16 16-byte words once and folds them (XOR) into
 // *sink with one atomic per wave, so that no load can be elided.  Each
 // workgroup streams one contiguous chunk, 64 KiB per round (eight coalesced
-// 8 KiB loads in flight per thread): a plain HBM read stream to compare the
-// streaming kernels with.
+// 8 KiB loads in flight per thread), with nontemporal loads (the fastest plain
+// stream measured on MI355X): the HBM read rate the streaming kernels are
+// compared with.
 // ---------------------------------------------------------------------------
 constexpr int kProbeThreads = 512;
 
@@ -561,11 +568,11 @@ __global__ __launch_bounds__(kProbeThreads) void read_probe_kernel(const u32x4* 
     for (; i + 7 * kProbeThreads < hi; i += 8 * kProbeThreads) {
         u32x4 v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = p[i + u * kProbeThreads];
+        for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(p + i + u * kProbeThreads);
 #pragma unroll
         for (int u = 0; u < 8; ++u) acc ^= v[u];
     }
-    for (; i < hi; i += kProbeThreads) acc ^= p[i];
+    for (; i < hi; i += kProbeThreads) acc ^= __builtin_nontemporal_load(p + i);
     uint32_t x = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) x ^= __shfl_xor(x, off, 64);
