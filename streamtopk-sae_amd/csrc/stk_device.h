@@ -1,11 +1,12 @@
 // stk_device.h -- device-side building blocks for the streaming top-k encoder
-// on gfx950 (CDNA4): sort keys, the MFMA score main loop, and the LDS layout
-// of the staged X tile.
+// on gfx950 (CDNA4): sort keys, the MFMA score main loops (MainLoop: W in
+// registers, 4 waves, used by group_kernel; TileStream: W and X staged in
+// LDS, 8 waves, used by main_kernel) and queue compaction helpers.
 //
-// Score layout.  A workgroup is 4 wavefronts of 64 lanes.  Each wavefront owns
-// FRAGS blocks of 32 latents (W rows, the MFMA "A" operand) and NB blocks of
-// 32 batch rows (X rows, the MFMA "B" operand), and accumulates the fp32
-// scores W_blk . X_blk^T with v_mfma_f32_32x32x{16 bf16|16 f16|2 f32}.
+// Score layout.  Each wavefront owns blocks of 32 latents (W rows, the MFMA
+// "A" operand) and NB blocks of 32 batch rows (X rows, the MFMA "B" operand),
+// and accumulates the fp32 scores W_blk . X_blk^T with
+// v_mfma_f32_32x32x{16 bf16|16 f16|2 f32}.
 //
 // Permuted reduction axis.  One "d-step" covers 128 bytes of every W row
 // (64 bf16/fp16 or 32 fp32 elements).  Lane l holds row (l % 32) of its block
@@ -216,218 +217,6 @@ struct MainLoop {
 };
 
 // ---------------------------------------------------------------------------
-// TileStream: the score main loop as one flat stream of d-steps over all the
-// tiles a workgroup owns.  A tile is 32*FRAGS*WAVES latents x 32*NB rows and
-// takes nds3 d-steps: the nds = d / DS real ones (d is a multiple of the
-// d-step) rounded up to a multiple of 3; the padding steps load a valid step
-// again and skip their MFMAs.  Three register sets of W (and of X) keep the
-// loads of the next two d-steps in flight -- across tile boundaries too.
-// Every load is unconditional (rows past F or B and steps past the end are
-// clamped to valid addresses; the scores they produce are never selected), so
-// the in-order vmcnt waits never drain the prefetched W loads.  X goes
-// through a ring of three LDS buffers (one barrier per d-step).
-//
-// run() calls epi(t, acc, bias) after the last d-step of tile t (0-based
-// within the workgroup's tiles) and then clears acc.  The epilogue may use LDS
-// other than the X buffers and the bias buffers and must neither issue global
-// loads nor spill registers (a scratch reload, like a global load, waits for
-// every older prefetched W load); the bias of tile t it receives comes from
-// LDS, stored there during the previous tile.
-// ---------------------------------------------------------------------------
-template <int DT, int NB, int FRAGS, int WAVES>
-struct TileStream {
-    static constexpr int DS = Dt<DT>::DS;
-    static constexpr int ES = Dt<DT>::esize;
-    static constexpr int kThr = 64 * WAVES;
-    static constexpr int kXTotal = 32 * NB * 8;                    // 16-byte X chunks per d-step
-    static constexpr int kXChunks = (kXTotal + kThr - 1) / kThr;   // per thread
-    static constexpr int kTileF = 32 * FRAGS * WAVES;             // latents per tile
-    static_assert(kXTotal % kThr == 0 || kXChunks == 1, "X chunk split");
-
-    const float* bias;
-    int64_t F;
-    int64_t tile_begin;
-    int ntiles, nds, nds3;
-    int tid, lane, wave, h, jl;
-    const unsigned char* W;
-    int64_t w_row_bytes;
-
-    // load cursor (uniform) and per-lane row pointers of the cursor's tile
-    int lt, ls;
-    const unsigned char* lw[FRAGS];
-    const unsigned char* lx[kXChunks];
-    bool xok[kXChunks];
-
-    __device__ __forceinline__ void init_x(const unsigned char* X, int64_t B, int64_t b0, int64_t d)
-    {
-#pragma unroll
-        for (int p = 0; p < kXChunks; ++p) {
-            const int c = tid + kThr * p;
-            const int row = (c >> 3) % (32 * NB), c16 = c & 7;
-            int64_t r = b0 + row;
-            r = (r < B) ? r : B - 1;
-            lx[p] = X + (r * d) * ES + c16 * 16;
-            xok[p] = c < kXTotal;
-        }
-    }
-
-    __device__ __forceinline__ void set_rows(int t)
-    {
-        const int64_t tile = tile_begin + (t < ntiles ? t : ntiles - 1);
-#pragma unroll
-        for (int a = 0; a < FRAGS; ++a) {
-            int64_t f = tile * kTileF + wave * (32 * FRAGS) + a * 32 + jl;
-            f = (f < F) ? f : F - 1;
-            lw[a] = W + f * w_row_bytes + h * 64;
-        }
-    }
-
-    __device__ __forceinline__ void issue(u32x4 (&xr)[kXChunks], u32x4 (&w)[FRAGS][4])
-    {
-        const int s = (lt >= ntiles || ls >= nds) ? nds - 1 : ls;
-        const int64_t so = (int64_t)s * kStepBytes;
-#pragma unroll
-        for (int p = 0; p < kXChunks; ++p) xr[p] = *(const u32x4*)(lx[p] + so);
-#pragma unroll
-        for (int a = 0; a < FRAGS; ++a) {
-            const unsigned char* pw = lw[a] + so;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) w[a][q] = *(const u32x4*)(pw + q * 16);
-        }
-        if (lt < ntiles && ++ls == nds3) {
-            ls = 0;
-            ++lt;
-            if (lt < ntiles) set_rows(lt);
-        }
-    }
-
-    __device__ __forceinline__ void store_x(const u32x4 (&xr)[kXChunks], unsigned char* xs) const
-    {
-#pragma unroll
-        for (int p = 0; p < kXChunks; ++p) {
-            const int c = tid + kThr * p;
-            const int row = c >> 3, c16 = c & 7;
-            if (kXTotal % kThr == 0 || xok[p]) *(u32x4*)(xs + row * kXRowStride + c16 * 16) = xr[p];
-        }
-    }
-
-    __device__ __forceinline__ void compute(f32x16 (&acc)[FRAGS][NB], const u32x4 (&w)[FRAGS][4],
-                                            const unsigned char* xs) const
-    {
-        // two 32-row blocks at a time: two independent accumulation chains
-        constexpr int NP = NB < 2 ? NB : 2;
-#pragma unroll
-        for (int n0 = 0; n0 < NB; n0 += NP) {
-            u32x4 bx[NP][4];
-#pragma unroll
-            for (int n = 0; n < NP; ++n)
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    bx[n][q] = *(const u32x4*)(xs + (32 * (n0 + n) + jl) * kXRowStride + h * 64 + q * 16);
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int n = 0; n < NP; ++n)
-#pragma unroll
-                    for (int a = 0; a < FRAGS; ++a) mfma_quad<DT>(acc[a][n0 + n], w[a][q], bx[n][q]);
-        }
-    }
-
-    // The bias goes through LDS (bias_lds: two kTileF-float buffers, by tile
-    // parity).  Wave 0 loads tile t+1's bias during tile t's d-steps and
-    // stores it to LDS within the same three-step iteration, so the compiler
-    // waits for those loads exactly (they are older than the step's own
-    // loads); the epilogue reads its bias from LDS and waits for no global
-    // load, so the prefetched W and X loads stay in flight across it.
-    __device__ __forceinline__ void bias_load(float (&bn)[kTileF / 64], int t) const
-    {
-        const int64_t f0 = (tile_begin + t) * kTileF + lane * (kTileF / 64);
-#pragma unroll
-        for (int e = 0; e < kTileF / 64; ++e) {
-            const int64_t f = f0 + e;
-            bn[e] = bias[(f < F) ? f : F - 1];
-        }
-    }
-
-    __device__ __forceinline__ void bias_store(const float (&bn)[kTileF / 64], float* buf) const
-    {
-#pragma unroll
-        for (int e = 0; e < kTileF / 64; ++e) buf[lane * (kTileF / 64) + e] = bn[e];
-    }
-
-    // Bias of this lane's latents: entry [a][r] is latent (within the tile)
-    // wave*32*FRAGS + a*32 + 8*(r/4) + 4*h + r%4.
-    __device__ __forceinline__ void bias_read(float (&bv)[FRAGS][16], const float* buf) const
-    {
-#pragma unroll
-        for (int a = 0; a < FRAGS; ++a)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const f32x4 v = *(const f32x4*)(buf + wave * (32 * FRAGS) + a * 32 + g * 8 + h * 4);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) bv[a][4 * g + e] = v[e];
-            }
-    }
-
-    template <class Epi>
-    __device__ __forceinline__ void run(f32x16 (&acc)[FRAGS][NB], unsigned char* xs0, unsigned char* xs1,
-                                        unsigned char* xs2, float* bias_lds, Epi epi)
-    {
-        if (ntiles <= 0) return;
-        lt = 0;
-        ls = 0;
-        set_rows(0);
-        u32x4 w0[FRAGS][4], w1[FRAGS][4], w2[FRAGS][4];
-        u32x4 x0[kXChunks], x1[kXChunks], x2[kXChunks];
-        if (wave == 0) {
-            float bn[kTileF / 64];
-            bias_load(bn, 0);
-            bias_store(bn, bias_lds);
-        }
-        issue(x0, w0);
-        issue(x1, w1);
-        issue(x2, w2);
-        store_x(x0, xs0);
-#pragma unroll
-        for (int a = 0; a < FRAGS; ++a)
-#pragma unroll
-            for (int n = 0; n < NB; ++n)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[a][n][r] = 0.f;
-        __syncthreads();
-        for (int t = 0; t < ntiles; ++t) {
-            float* bnext = bias_lds + ((t + 1) & 1) * kTileF;
-            for (int s = 0; s < nds3; s += 3) {
-                float bn[kTileF / 64];
-                if (wave == 0) bias_load(bn, t + 1);   // past the last tile: clamped, unused
-                store_x(x1, xs1);
-                if (s < nds) compute(acc, w0, xs0);
-                issue(x0, w0);
-                __syncthreads();
-                store_x(x2, xs2);
-                if (s + 1 < nds) compute(acc, w1, xs1);
-                issue(x1, w1);
-                __syncthreads();
-                store_x(x0, xs0);
-                if (s + 2 < nds) compute(acc, w2, xs2);
-                issue(x2, w2);
-                if (wave == 0) bias_store(bn, bnext);
-                __syncthreads();
-            }
-            float bv[FRAGS][16];
-            bias_read(bv, bias_lds + (t & 1) * kTileF);
-            epi(t, acc, bv);
-#pragma unroll
-            for (int a = 0; a < FRAGS; ++a)
-#pragma unroll
-                for (int n = 0; n < NB; ++n)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[a][n][r] = 0.f;
-        }
-    }
-};
-
-// ---------------------------------------------------------------------------
 // Compacts the queue segments (in global memory) of this wave's rows that are
 // full to their top-k: rows wave*R .. wave*R + R - 1 (R <= 64), segment of
 // row r at qrow(r), cap keys; cnt and thr in LDS.  Segment keys are read
@@ -512,7 +301,7 @@ __device__ __forceinline__ uint64_t compact_row(uint64_t* q, int n, uint64_t* sc
 }
 
 // ---------------------------------------------------------------------------
-// TileStream2: the score main loop with both operands staged in LDS.  A tile
+// TileStream: the score main loop with both operands staged in LDS.  A tile
 // is 32*WAVES latents x 32*NB rows and takes nds2 d-steps: the nds real ones
 // rounded up to even (a padding step loads a valid step again and skips its
 // MFMAs).
@@ -535,12 +324,15 @@ __device__ __forceinline__ uint64_t compact_row(uint64_t* q, int n, uint64_t* sc
 // may issue a data-dependent number of global stores, which the compiler
 // cannot count, and the wait restores its exact counts for the d-step loop
 // (the prefetched loads it includes have had the whole epilogue to land).
-// The epilogue may use LDS other than the rings and the bias buffers.  The
-// bias of tile t comes from LDS: wave 0 loads the next tile's bias inside the
-// d-step loop and stores it within the same iteration.
+// The epilogue may use LDS other than ring buffer 0 (which holds the next
+// tile's first step) and the bias buffers.  Ring buffer 1 (W and X) is idle
+// during it: its last readers passed the tile's last barrier and its next
+// writer runs after the epilogue, so an epilogue that uses it must end with a
+// workgroup barrier.  The bias of tile t comes from LDS: wave 0 loads the next
+// tile's bias inside the d-step loop and stores it within the same iteration.
 // ---------------------------------------------------------------------------
 template <int DT, int NB, int WAVES>
-struct TileStream2 {
+struct TileStream {
     static constexpr int DS = Dt<DT>::DS;
     static constexpr int ES = Dt<DT>::esize;
     static constexpr int kThr = 64 * WAVES;

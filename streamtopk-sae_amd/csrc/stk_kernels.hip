@@ -95,7 +95,7 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
     constexpr int BT = 32 * NB;
     constexpr int WAVES = kMainWaves;
     constexpr int R = BT / WAVES;   // rows each wave spills and flushes
-    using TS = TileStream2<DT, NB, WAVES>;
+    using TS = TileStream<DT, NB, WAVES>;
     extern __shared__ __align__(16) unsigned char smem[];
     const int cap = a.cap, lq = a.lq;
     uint64_t* thr = (uint64_t*)(smem + TS::kRingBytes);          // [BT] row threshold keys
@@ -585,7 +585,7 @@ __global__ __launch_bounds__(kProbeThreads) void read_probe_kernel(const u32x4* 
 size_t main_lds_bytes(int NB, int cap, int lq)
 {
     const size_t BT = 32 * (size_t)NB;
-    const size_t rings = 2 * (size_t)kTileLatents * kXRowStride + 2 * BT * kXRowStride;   // TileStream2
+    const size_t rings = 2 * (size_t)kTileLatents * kXRowStride + 2 * BT * kXRowStride;   // TileStream rings
     return rings + BT * 8 + BT * 8 + 2 * kTileLatents * 4 + BT * (size_t)lq * 8 + (size_t)kMainWaves * cap * 8;
 }
 
