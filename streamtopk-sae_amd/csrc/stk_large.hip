@@ -1,20 +1,26 @@
 // stk_large.hip -- the streaming kernel for large batches (compute-bound).
 //
 // mainl_kernel: one workgroup of 4 waves (one per SIMD, up to 512 registers
-// each) owns 256 rows and a contiguous range of 256-latent tiles.  Each wave
-// scores 64 latents x 256 rows per tile: 2 x 8 blocks of
-// v_mfma_f32_32x32x16 with the 256 accumulators per lane in AGPRs, so every W
-// byte fetched feeds 256 rows and every staged X byte feeds 256 latents.
-//   - W: straight from global memory into registers, 2 d-steps ahead; each
-//     16-byte quad is reloaded as soon as its last MFMA of the step issued.
-//     The pipeline restarts at every tile, so the epilogue holds no prefetch.
-//   - X: 256 rows x 128 bytes per d-step, 2 d-steps ahead in registers, then
-//     through a 2-buffer LDS ring (one barrier per d-step).
+// each) owns 256 rows and a contiguous range of 256-latent tiles.  The waves
+// form a 2 x 2 grid: each scores 128 latents x 128 rows per tile as 4 x 4
+// blocks of v_mfma_f32_32x32x16, with the 256 accumulators per lane in AGPRs.
+// Both operands come from LDS; each 16-byte operand read feeds 4 MFMAs.
+//   - W and X: whole 128-byte lines from global memory into registers, 2
+//     d-steps ahead, then into 2-stage LDS rings (W: 144-byte row stride; X:
+//     128-byte rows with the 16-byte chunks swizzled) that the MFMA-layout
+//     reads hit without bank conflicts.  One barrier per d-step.  The W lines
+//     are shared through L2 by the row blocks of the W range.
+//   - The next step's LDS stores and the loads two steps ahead are spread
+//     through the MFMA stream (one per MFMA), not issued as a burst: with
+//     one wave per SIMD, a blocked vector-memory issue stalls the MFMAs.
+//   - The pipeline restarts at every tile, so the epilogue holds no prefetch.
 //   - bias: the tile's 256 values are loaded at the tile start and staged in
 //     LDS for the epilogue.
-//   - epilogue: scores not below the row threshold are appended to the row's
-//     queue segment in global memory (counters in LDS).  A full segment is
-//     rank-compacted to its top-k, which raises the row threshold.
+//   - epilogue, one row block at a time: the accumulators are read once,
+//     biased, compared with the row threshold and staged in LDS; survivors
+//     go to the row's queue segment in global memory (counters in LDS).  A
+//     full segment is rank-compacted to its top-k, which raises the row
+//     threshold.
 //   - grid: workgroups are placed so that the row blocks sharing a W range
 //     run on one XCD (workgroup i runs on XCD i % 8), and W is fetched into
 //     that XCD's L2 once for all of them.
@@ -31,10 +37,17 @@ namespace stk {
 namespace {
 
 constexpr int kLWaves = 4;
-constexpr int kLNB = 8;                      // 32-row blocks per workgroup
-constexpr int kLFrags = 2;                   // 32-latent fragments per wave
-constexpr int kLTile = 32 * kLFrags * kLWaves;   // 256 latents per tile
-constexpr int kLXChunks = kLargeRows * 8 / kLargeThreads;   // 16-byte X chunks per thread per d-step
+// The waves form a 2 x 2 grid over the 256 x 256 tile: wave w scores latents
+// (w & 1) * 128 .. +127 for rows (w >> 1) * 128 .. +127, as 4 x 4 blocks of
+// 32 x 32.  Each operand block read from LDS feeds 4 MFMAs.
+constexpr int kLNB = 4;                      // 32-row blocks per wave
+constexpr int kLFrags = 4;                   // 32-latent fragments per wave
+constexpr int kLTile = 256;                  // latents per tile
+static_assert(2 * 32 * kLFrags == kLTile && 2 * 32 * kLNB == kLargeRows, "2 x 2 wave grid");
+constexpr int kLWChunks = kLTile * 8 / kLargeThreads;       // 16-byte W chunks per thread per d-step
+constexpr int kLWStage = kLTile * kXRowStride;              // W ring stage: 256 rows x 144 B (padded)
+constexpr int kLXStage = kLargeRows * kStepBytes;           // X ring stage: 256 rows x 128 B (swizzled)
+constexpr int kLXChunks = kLargeRows * 8 / kLargeThreads;  // 16-byte X chunks per thread per d-step
 
 // Buffer resource (raw, gfx9 family): loads at byte offsets >= num_records
 // return zeros, which bounds rows past B and latents past F, and a zero-length
@@ -43,6 +56,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
 {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_records, 0x00020000);
 }
+
+// X ring layout: row r's 16-byte chunk c sits in slot c ^ ((r >> 1) & 7) of the
+// row's 128 bytes, so that the MFMA-layout reads (32 rows x one chunk per
+// half-wave) hit 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int xswz(int r) { return (r >> 1) & 7; }
 
 template <int DT, bool SAMPLE>
 struct BigStream {
@@ -56,22 +74,24 @@ struct BigStream {
     int samp_log2;               // SAMPLE: tile t covers sampled latents t*256 ..
     int tid, lane, wave, h, jl;
 
-    // W and X cursors (tile, step), uniform; a tile's pipeline ends at the tile
-    int wt, ws, xt, xsn;
-    __amdgpu_buffer_rsrc_t wres, xres, zres;
-    int wvoff[kLFrags];          // row of this lane's latent within the tile, + lane half
-    int xvoff[kLXChunks];        // row of this thread's X chunk within the row block
+    // load cursors (absolute d-steps), uniform
+    int ws, xs;
+    __amdgpu_buffer_rsrc_t wres[4], xres, zres;   // W: one resource per 64-row run of the tile
+    int wvoff[kLWChunks];        // W chunk p of this thread: offset within its run
+    int xvoff[kLXChunks];        // X chunk p of this thread: source offset within the row block
+    int xrd[4];                  // X operand read offset of quad q (row jl of block 0)
 
     __device__ __forceinline__ void init()
     {
-        // encode: offsets within the tile; sample: within this wave's 64-latent
-        // run of a sampled block (its own resource base)
-        const int wbase = SAMPLE ? 0 : wave * (32 * kLFrags);
+        // W chunk p: row (tid >> 3) + 32 p of the tile, 16-byte column tid & 7
 #pragma unroll
-        for (int a = 0; a < kLFrags; ++a)
-            wvoff[a] = (wbase + a * 32 + jl) * (int)row_bytes + h * 64;
+        for (int p = 0; p < kLWChunks; ++p)
+            wvoff[p] = (((tid >> 3) + 32 * p) & 63) * (int)row_bytes + (tid & 7) * 16;
+        // X chunk p: row (tid >> 3) + 32 p of the row block, 16-byte column tid & 7
 #pragma unroll
         for (int p = 0; p < kLXChunks; ++p) xvoff[p] = ((tid >> 3) + 32 * p) * (int)row_bytes + (tid & 7) * 16;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xrd[q] = jl * kStepBytes + (((h * 4 + q) ^ xswz(jl)) * 16);
         const int64_t nrows = (B - b0 < kLargeRows) ? B - b0 : kLargeRows;
         xres = make_rsrc(X + b0 * row_bytes, nrows * row_bytes);
         zres = make_rsrc(X, 0);
@@ -79,109 +99,125 @@ struct BigStream {
 
     __device__ __forceinline__ void begin_tile(int t)
     {
-        wt = xt = t;
-        ws = xsn = s_lo;
-        set_w_tile(t);
-    }
-
-    __device__ __forceinline__ void set_w_tile(int t)
-    {
+        ws = xs = s_lo;
         const int64_t tile0 = (tile_begin + t) * kLTile;
-        if (SAMPLE) {
-            // the wave's 64 sampled latents are consecutive latents of one block
-            const int64_t f0 = sample_latent(tile0 + wave * (32 * kLFrags), samp_log2);
-            wres = make_rsrc(W + f0 * row_bytes, (int64_t)(32 * kLFrags) * row_bytes);
-        } else {
-            int64_t n = F - tile0;
-            n = n < kLTile ? (n > 0 ? n : 0) : kLTile;
-            wres = make_rsrc(W + tile0 * row_bytes, n * row_bytes);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (SAMPLE) {
+                // each 64-row run is 64 consecutive latents of one sampled block
+                const int64_t f0 = sample_latent(tile0 + 64 * j, samp_log2);
+                wres[j] = make_rsrc(W + f0 * row_bytes, (int64_t)64 * row_bytes);
+            } else {
+                const int64_t f0 = tile0 + 64 * j;
+                int64_t n = F - f0;
+                n = n < 64 ? (n > 0 ? n : 0) : 64;
+                wres[j] = make_rsrc(W + (n > 0 ? f0 : 0) * row_bytes, n * row_bytes);
+            }
         }
     }
 
-    // Resource and step offset of the W cursor's step; advances the cursor.
-    __device__ __forceinline__ void next_w(__amdgpu_buffer_rsrc_t& r, int& so)
+    // W of step ws (zeros past s_hi) into registers, whole 128-byte lines.
+    __device__ __forceinline__ void issue_w(u32x4 (&w)[kLWChunks])
     {
-        const bool live = wt < ntiles && ws < s_hi;
-        r = live ? wres : zres;
-        so = live ? ws * kStepBytes : 0;
+        const bool live = ws < s_hi;
+        const int so = live ? ws * kStepBytes : 0;
+#pragma unroll
+        for (int p = 0; p < kLWChunks; ++p)
+            w[p] = __builtin_amdgcn_raw_buffer_load_b128(live ? wres[p >> 1] : zres, wvoff[p], so, 0);
         ++ws;
     }
 
-    __device__ __forceinline__ void load_wq(u32x4 (&w)[kLFrags][4], int q, __amdgpu_buffer_rsrc_t r, int so) const
+    __device__ __forceinline__ void store_w(const u32x4 (&w)[kLWChunks], unsigned char* wst) const
     {
 #pragma unroll
-        for (int a = 0; a < kLFrags; ++a) w[a][q] = __builtin_amdgcn_raw_buffer_load_b128(r, wvoff[a] + q * 16, so, 0);
+        for (int p = 0; p < kLWChunks; ++p)
+            *(u32x4*)(wst + ((tid >> 3) + 32 * p) * kXRowStride + (tid & 7) * 16) = w[p];
     }
 
-    __device__ __forceinline__ void issue_w(u32x4 (&w)[kLFrags][4])
-    {
-        __amdgpu_buffer_rsrc_t r;
-        int so;
-        next_w(r, so);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) load_wq(w, q, r, so);
-    }
-
+    // X of step xs (zeros past s_hi and for rows past B) into registers, whole lines.
     __device__ __forceinline__ void issue_x(u32x4 (&x)[kLXChunks])
     {
-        const bool live = xt < ntiles && xsn < s_hi;
+        const bool live = xs < s_hi;
         const __amdgpu_buffer_rsrc_t r = live ? xres : zres;
-        const int so = live ? xsn * kStepBytes : 0;
+        const int so = live ? xs * kStepBytes : 0;
 #pragma unroll
         for (int p = 0; p < kLXChunks; ++p) x[p] = __builtin_amdgcn_raw_buffer_load_b128(r, xvoff[p], so, 0);
-        ++xsn;
+        ++xs;
     }
 
-    __device__ __forceinline__ void store_x(const u32x4 (&x)[kLXChunks], unsigned char* xs) const
+    // Row r's chunk c goes to slot c ^ xswz(r) of the row's 128 bytes.
+    __device__ __forceinline__ void store_x(const u32x4 (&x)[kLXChunks], unsigned char* xst) const
     {
 #pragma unroll
-        for (int p = 0; p < kLXChunks; ++p)
-            *(u32x4*)(xs + ((tid >> 3) + 32 * p) * kXRowStride + (tid & 7) * 16) = x[p];
+        for (int p = 0; p < kLXChunks; ++p) {
+            const int r = (tid >> 3) + 32 * p;
+            *(u32x4*)(xst + r * kStepBytes + (((tid & 7) ^ xswz(r)) * 16)) = x[p];
+        }
     }
 
-    // One d-step.  The X operands of all 8 row blocks for quad q + 1 are read
-    // from LDS while the 16 MFMAs of quad q run; after them, quad q of this
-    // wave's W is reloaded with the step two ahead (its last use has issued).
-    // One d-step on LDS buffer `xs`.  Each quad interleaves its 16 MFMAs with
-    // the 8 LDS reads of the next quad and the reloads of its own W registers,
-    // so those issue while an MFMA executes: the MFMAs of fragment 0 come
-    // first (reads interleaved), then fragment 1, with fragment 0's W reload
-    // issued among them.
-    __device__ __forceinline__ void step(f32x16 (&acc)[kLFrags][kLNB], u32x4 (&w)[kLFrags][4],
-                                         const unsigned char* xs)
+    // One d-step from LDS stages wst / xst, with the next step's staging folded
+    // into the MFMA stream: W(s+1) and X(s+1) go from registers into the other
+    // stages (wnx / xnx) during quads 0 and 1, and their registers are reloaded
+    // with W(s+3) / X(s+3) during quads 2 and 3.  One vector-memory or LDS-write
+    // instruction sits between MFMAs, so the texture path and the LDS work in
+    // the background instead of stalling the wave's in-order issue.  Each quad
+    // also reads the 8 operand blocks (4 W fragments, 4 X blocks) of the next.
+    __device__ __forceinline__ void step(f32x16 (&acc)[kLFrags][kLNB], const unsigned char* wst,
+                                         const unsigned char* xst, u32x4 (&wr)[kLWChunks],
+                                         u32x4 (&xr)[kLXChunks], unsigned char* wnx, unsigned char* xnx)
     {
-        __amdgpu_buffer_rsrc_t r;
-        int so;
-        next_w(r, so);
-        const unsigned char* xl = xs + jl * kXRowStride + h * 64;
-        u32x4 bA[kLNB], bB[kLNB];
+        const unsigned char* wl = wst + ((wave & 1) * (32 * kLFrags) + jl) * kXRowStride + h * 64;
+        const unsigned char* xl = xst + (wave >> 1) * (32 * kLNB) * kStepBytes;
+        u32x4 bA[kLNB], bB[kLNB], aA[kLFrags], aB[kLFrags];
 #pragma unroll
-        for (int n = 0; n < kLNB; ++n) bA[n] = *(const u32x4*)(xl + (32 * n) * kXRowStride);
+        for (int n = 0; n < kLNB; ++n) bA[n] = *(const u32x4*)(xl + xrd[0] + (32 * n) * kStepBytes);
+#pragma unroll
+        for (int fa = 0; fa < kLFrags; ++fa) aA[fa] = *(const u32x4*)(wl + (32 * fa) * kXRowStride);
         __builtin_amdgcn_sched_barrier(0);   // quad 0's operands are all in flight before any MFMA
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             u32x4 (&cur)[kLNB] = (q & 1) ? bB : bA;
             u32x4 (&nxt)[kLNB] = (q & 1) ? bA : bB;
+            u32x4 (&wc)[kLFrags] = (q & 1) ? aB : aA;
+            u32x4 (&wn)[kLFrags] = (q & 1) ? aA : aB;
             if (q < 3) {
 #pragma unroll
-                for (int n = 0; n < kLNB; ++n) nxt[n] = *(const u32x4*)(xl + (32 * n) * kXRowStride + (q + 1) * 16);
+                for (int fa = 0; fa < kLFrags; ++fa)
+                    wn[fa] = *(const u32x4*)(wl + (32 * fa) * kXRowStride + (q + 1) * 16);
+#pragma unroll
+                for (int n = 0; n < kLNB; ++n) nxt[n] = *(const u32x4*)(xl + xrd[q + 1] + (32 * n) * kStepBytes);
             }
 #pragma unroll
-            for (int n = 0; n < kLNB; ++n) mfma_quad<DT>(acc[0][n], w[0][q], cur[n]);
-            w[0][q] = __builtin_amdgcn_raw_buffer_load_b128(r, wvoff[0] + q * 16, so, 0);
+            for (int fa = 0; fa < kLFrags; ++fa)
 #pragma unroll
-            for (int n = 0; n < kLNB; ++n) mfma_quad<DT>(acc[1][n], w[1][q], cur[n]);
-            w[1][q] = __builtin_amdgcn_raw_buffer_load_b128(r, wvoff[1] + q * 16, so, 0);
-            // pattern: (MFMA, DS read) x 8, (MFMA, VMEM read), MFMA x 7, then the last VMEM
+                for (int n = 0; n < kLNB; ++n) mfma_quad<DT>(acc[fa][n], wc[fa], cur[n]);
+            if (q == 0) store_w(wr, wnx);
+            if (q == 1) store_x(xr, xnx);
+            if (q == 2) issue_w(wr);
+            if (q == 3) issue_x(xr);
+            // (MFMA, DS read) x 8 then (MFMA, staging op) x 8; quad 3: (MFMA, VMEM) x 8, MFMA x 8
+            if (q < 3) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                if (q < 3) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+                for (int i = 0; i < 8; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    if (q < 2)
+                        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // DS write
+                    else
+                        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM read
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM read
-            __builtin_amdgcn_sched_group_barrier(0x008, 7, 0);
-            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -201,7 +237,7 @@ __device__ __forceinline__ float agpr_read(float x)
 
 size_t mainl_lds_bytes(int cap)
 {
-    return 2 * (size_t)kLargeRows * kXRowStride + kLTile * sizeof(float) + kLargeRows * 8 + kLargeRows * 4 +
+    return 2 * (size_t)kLWStage + 2 * (size_t)kLXStage + kLTile * sizeof(float) + kLargeRows * 8 + kLargeRows * 4 +
            (size_t)kLWaves * cap * 8 + (size_t)kLargeRows * sizeof(uint64_t*);
 }
 
@@ -209,9 +245,11 @@ template <int DT, bool SAMPLE>
 __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
 {
     extern __shared__ __align__(16) unsigned char smem[];
-    unsigned char* xs0 = smem;
-    unsigned char* xs1 = smem + kLargeRows * kXRowStride;
-    float* bias_s = (float*)(smem + 2 * kLargeRows * kXRowStride);   // [kLTile]
+    unsigned char* wst0 = smem;                                       // W ring
+    unsigned char* wst1 = smem + kLWStage;
+    unsigned char* xs0 = smem + 2 * kLWStage;                         // X ring (swizzled)
+    unsigned char* xs1 = xs0 + kLXStage;
+    float* bias_s = (float*)(xs1 + kLXStage);                         // [kLTile]
     uint64_t* thr = (uint64_t*)(bias_s + kLTile);                    // [rows]
     int* cnt = (int*)(thr + kLargeRows);                              // [rows]
     uint64_t** qrow = (uint64_t**)(cnt + kLargeRows);                 // [rows] segment of each row
@@ -220,6 +258,8 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, jl = lane & 31;
+    const int lw0 = (wave & 1) * (32 * kLFrags);   // this wave's first latent of the tile
+    const int rw0 = (wave >> 1) * (32 * kLNB);     // this wave's first row of the row block
 
     // workgroup -> (row block, W range): the row blocks of a W range share an XCD.
     // Sample mode: workgroup -> (row block, sample tile, d range).
@@ -283,7 +323,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
 
     if (bs.ntiles > 0) {
         bs.init();
-        u32x4 wA[kLFrags][4], wB[kLFrags][4];
+        u32x4 wA[kLWChunks], wB[kLWChunks];
         u32x4 xA[kLXChunks], xB[kLXChunks];
 
         f32x16 acc[kLFrags][kLNB];
@@ -303,37 +343,40 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                 const int64_t f = tile0 + tid;
                 bnext = a.bias[f < F ? f : F - 1];
             }
+            // Per d-step: W and X two steps ahead in registers, then 2-stage LDS
+            // rings (W padded, X swizzled); one barrier per d-step.  Loads past
+            // the last step read zeros.
             bs.begin_tile(t);
-            bs.issue_w(wA);
-            bs.issue_w(wB);
-            bs.issue_x(xA);
-            bs.issue_x(xB);
+            bs.issue_w(wA);   // W(0)
+            bs.issue_x(xA);   // X(0)
+            bs.issue_w(wB);   // W(1)
+            bs.issue_x(xB);   // X(1)
+            bs.store_w(wA, wst0);
             bs.store_x(xA, xs0);
-            bs.issue_x(xA);
-            __syncthreads();
+            bs.issue_w(wA);   // W(2)
+            bs.issue_x(xA);   // X(2)
             // a padded last step (s >= nds) reads zeros: every step computes unconditionally
             for (int s = 0; s < bs.nds2; s += 2) {
-                bs.step(acc, wA, xs0);
-                bs.store_x(xB, xs1);
-                bs.issue_x(xB);
+                __syncthreads();   // step s in stage 0; stage 1 was last read in step s-1
+                bs.step(acc, wst0, xs0, wB, xB, wst1, xs1);   // stages W/X(s+1), loads W/X(s+3)
                 __syncthreads();
-                bs.step(acc, wB, xs1);
-                bs.store_x(xA, xs0);
-                bs.issue_x(xA);
-                __syncthreads();
+                bs.step(acc, wst1, xs1, wA, xA, wst0, xs0);   // stages W/X(s+2), loads W/X(s+4)
             }
+            // the loads past the last step (zeros) land before the rings are reused
+            __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0)
+            __syncthreads();
             if (SAMPLE) {
                 // raw partial scores of this d range: P[ks][row][sample index]
                 float* P = a.P + (int64_t)ks * B * a.nsamp;
 #pragma unroll
                 for (int n = 0; n < kLNB; ++n) {
-                    const int64_t row = b0 + 32 * n + jl;
+                    const int64_t row = b0 + rw0 + 32 * n + jl;
                     if (row < B) {
 #pragma unroll
                         for (int fa = 0; fa < kLFrags; ++fa)
 #pragma unroll
                             for (int r4 = 0; r4 < 4; ++r4) {
-                                const int64_t i = tile0 + wave * 64 + fa * 32 + r4 * 8 + h * 4;
+                                const int64_t i = tile0 + lw0 + fa * 32 + r4 * 8 + h * 4;
                                 f32x4 v;
 #pragma unroll
                                 for (int e = 0; e < 4; ++e) v[e] = acc[fa][n][r4 * 4 + e];
@@ -347,112 +390,89 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
             __syncthreads();
 
             // ---- epilogue: bias, threshold filter, append to the row segments ----
-            uint32_t vmask[kLFrags];
-            {
-                const bool edge = tile0 + kLTile > F ||
-                                  (a.sampled && (is_sampled(tile0, a.samp_log2, a.samp_blocks) ||
-                                                 is_sampled(tile0 + kLTile - 1, a.samp_log2, a.samp_blocks)));
+            // One row block at a time.  Its 64 scores per lane are read from the
+            // accumulators once, in straight-line code, biased and compared with
+            // the row threshold; they go to this wave's LDS staging area ([bit]
+            // [lane], in the idle W ring), where the survivor walk and any
+            // recheck read them back.  Bit 16*fa + r of a row mask is latent
+            // lat0 + fa*32 + 8*(r/4) + r%4; this lane's row is rw0 + 32*n + jl.
+            const bool edge = tile0 + kLTile > F ||
+                              (a.sampled && (is_sampled(tile0, a.samp_log2, a.samp_blocks) ||
+                                             is_sampled(tile0 + kLTile - 1, a.samp_log2, a.samp_blocks)));
+            const int lat0 = (int)tile0 + lw0 + h * 4;
+            const float* bias_l = bias_s + lw0 + h * 4;   // + fa*32 + 8*(r/4) + r%4
+            // latents past F or in the sample are never candidates here
+            uint64_t vmask = ~0ull;
+            if (edge) {
+                vmask = 0;
 #pragma unroll
-                for (int fa = 0; fa < kLFrags; ++fa) {
-                    uint32_t m = 0xFFFFu;
-                    if (edge) {
-                        m = 0;
-                        const int64_t fl = tile0 + wave * 64 + fa * 32 + h * 4;
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int64_t f = fl + (r >> 2) * 8 + (r & 3);
-                            const bool ok = f < F && !(a.sampled && is_sampled(f, a.samp_log2, a.samp_blocks));
-                            m |= ok ? (1u << r) : 0u;
-                        }
-                    }
-                    vmask[fa] = m;
+                for (int bit = 0; bit < 16 * kLFrags; ++bit) {
+                    const int64_t f = lat0 + (bit >> 4) * 32 + ((bit & 15) >> 2) * 8 + (bit & 3);
+                    const bool ok = f < F && !(a.sampled && is_sampled(f, a.samp_log2, a.samp_blocks));
+                    vmask |= ok ? (1ull << bit) : 0ull;
                 }
             }
-            // Scores are read from the accumulators (AGPRs) at each use and the
-            // bias of this lane's 32 latents is held in VGPRs; the prefetch
-            // registers are dead here.
-            // Latent of bit 16*fa + r of a row mask: lat0 + fa*32 + 8*(r/4) + r%4.
-            const int lat0 = (int)tile0 + wave * 64 + h * 4;
-            float bl[kLFrags * 16];
-#pragma unroll
-            for (int fa = 0; fa < kLFrags; ++fa)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) bl[fa * 16 + r] = bias_s[wave * 64 + h * 4 + fa * 32 + (r >> 2) * 8 + (r & 3)];
-            uint32_t pend[kLNB];
+            float* stage = (float*)wst0 + wave * (16 * kLFrags * 64);
 #pragma unroll
             for (int n = 0; n < kLNB; ++n) {
-                const int j = 32 * n + jl;
-                const uint64_t tk = thr[j];
-                const float tv = tk ? key_value(tk) : -__builtin_inff();
-                uint32_t m = 0;
+                const int row = rw0 + 32 * n + jl;
+                uint64_t pend = 0;
+                {
+                    const uint64_t tk = thr[row];
+                    const float tv = tk ? key_value(tk) : -__builtin_inff();
 #pragma unroll
-                for (int fa = 0; fa < kLFrags; ++fa)
+                    for (int fa = 0; fa < kLFrags; ++fa) {
+                        const f32x4 b0v = *(const f32x4*)(bias_l + fa * 32);
+                        const f32x4 b1v = *(const f32x4*)(bias_l + fa * 32 + 8);
+                        const f32x4 b2v = *(const f32x4*)(bias_l + fa * 32 + 16);
+                        const f32x4 b3v = *(const f32x4*)(bias_l + fa * 32 + 24);
+                        uint32_t m = 0;
 #pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        m |= (!(agpr_read(acc[fa][n][r]) + bl[fa * 16 + r] < tv)) ? (1u << (16 * fa + r)) : 0u;
-                m &= vmask[0] | (vmask[1] << 16);
-                pend[n] = (b0 + j < B) ? m : 0u;
-            }
-            for (int it = 0; it < 1 << 20; ++it) {
-                bool overflow = false;
-                // reserve the slots of every row block first, then wait once
-                int base[kLNB];
-#pragma unroll
-                for (int n = 0; n < kLNB; ++n)
-                    base[n] = pend[n] ? atomicAdd(&cnt[32 * n + jl], __builtin_popcount(pend[n])) : 0;
-                __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
-                // Per row block: the 32 biased scores of every lane go to this
-                // wave's LDS staging area (the X buffers are idle here), then each
-                // lane walks only its own set bits and reads each score back by
-                // address: max-popcount iterations instead of 32 divergent blocks.
-                float* stage = (float*)xs0 + wave * (kLFrags * 16 * 64);
-#pragma unroll
-                for (int n = 0; n < kLNB; ++n) {
-                    const uint32_t m = pend[n];
-                    if (__ballot(m != 0) == 0) continue;
-#pragma unroll
-                    for (int fa = 0; fa < kLFrags; ++fa)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r)
-                            stage[(fa * 16 + r) * 64 + lane] = agpr_read(acc[fa][n][r]) + bl[fa * 16 + r];
-                    uint64_t* q = qrow[32 * n + jl];
-                    uint32_t keep = 0, mm = m;
-                    int slot = base[n];
+                        for (int r = 0; r < 16; ++r) {
+                            const f32x4 bv = (r < 4) ? b0v : (r < 8) ? b1v : (r < 12) ? b2v : b3v;
+                            const float v = agpr_read(acc[fa][n][r]) + bv[r & 3];
+                            stage[(fa * 16 + r) * 64 + lane] = v;
+                            m |= (!(v < tv)) ? (1u << r) : 0u;
+                        }
+                        pend |= (uint64_t)m << (16 * fa);
+                    }
+                }
+                pend = (b0 + row < B) ? (pend & vmask) : 0ull;
+                uint64_t* q = qrow[row];
+                for (int it = 0; it < 1 << 20; ++it) {
+                    const int base = pend ? atomicAdd(&cnt[row], __popcll(pend)) : 0;
+                    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+                    // each lane walks only its own set bits and reads each score back by address
+                    uint64_t keep = 0, mm = pend;
+                    int slot = base;
                     while (mm) {
-                        const int bit = __builtin_ctz(mm);
+                        const int bit = __builtin_ctzll(mm);
                         mm &= mm - 1u;
                         if (slot < cap) {
                             const int off = (bit >> 4) * 32 + ((bit & 15) >> 2) * 8 + (bit & 3);
                             q[slot] = make_key(stage[bit * 64 + lane], lat0 + off);
                         } else {
-                            keep |= 1u << bit;
+                            keep |= 1ull << bit;
                         }
                         ++slot;
                     }
-                    pend[n] = keep;
-                    overflow |= keep != 0;
-                }
-                if (!__syncthreads_or(overflow)) break;
-                __threadfence_block();   // this thread's segment stores are complete
-                __syncthreads();
-                compact_full_rows<kLargeRows / kLWaves>(cnt, thr, cscr + wave * cap,
-                                                       [&](int r) { return qrow[r]; }, cap, k, wave, lane);
-                __threadfence_block();
-                __syncthreads();
-#pragma unroll
-                for (int n = 0; n < kLNB; ++n) {
-                    if (pend[n] == 0) continue;
-                    const uint64_t tk = thr[32 * n + jl];
-#pragma unroll
-                    for (int fa = 0; fa < kLFrags; ++fa)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int bit = 16 * fa + r;
-                            const int off = fa * 32 + (r >> 2) * 8 + (r & 3);
-                            if ((pend[n] >> bit & 1u) &&
-                                !(make_key(agpr_read(acc[fa][n][r]) + bl[fa * 16 + r], lat0 + off) > tk))
-                                pend[n] &= ~(1u << bit);
-                        }
+                    pend = keep;
+                    if (!__syncthreads_or(keep != 0)) break;
+                    __threadfence_block();   // this thread's segment stores are complete
+                    __syncthreads();
+                    compact_full_rows<kLargeRows / kLWaves>(cnt, thr, cscr + wave * cap,
+                                                           [&](int r) { return qrow[r]; }, cap, k, wave, lane);
+                    __threadfence_block();
+                    __syncthreads();
+                    // drop pending scores that fell below the raised threshold
+                    const uint64_t tk = thr[row];
+                    uint64_t mm2 = pend;
+                    while (mm2) {
+                        const int bit = __builtin_ctzll(mm2);
+                        mm2 &= mm2 - 1u;
+                        const int off = (bit >> 4) * 32 + ((bit & 15) >> 2) * 8 + (bit & 3);
+                        if (!(make_key(stage[bit * 64 + lane], lat0 + off) > tk)) pend &= ~(1ull << bit);
+                    }
                 }
             }
 #pragma unroll
