@@ -71,6 +71,47 @@ def cpu_baseline(X, W, b, k, seconds):
                       f"inputs), {t:.1f} s; oracle/stk_oracle_cpu.c, the reference streamtopk_cpu.cpp restated"}
 
 
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_c0_baseline():
+    """BASELINE config 0 (fp32 B=32 d=768 F=16384 k=32) on the product's own
+    OpenMP CPU encoder (stk_cpu_forward, the topk_sae_cpu path): 1 warmup call,
+    then the median of 5, on one thread (the reference CPU kernel is serial)
+    and on all of this process's cores."""
+    import ctypes
+    import statistics
+    import torch
+    from streamtopk_sae import _lib, make_inputs
+    lib = _lib.load()
+    B, d, F, k = 32, 768, 16384, 32
+    X, W, b = make_inputs(B, d, F, dtype=torch.float32, seed=0, device="cpu")
+    V = torch.empty(B, k, dtype=torch.float32)
+    I = torch.empty(B, k, dtype=torch.int32)
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())
+    res = {}
+    for nt in sorted({1, _cpu_cores()}):
+        times = []
+        for it in range(6):
+            t0 = time.perf_counter()
+            _lib.check(lib.stk_cpu_forward(ptr(X), ptr(W), ptr(b), ptr(V), ptr(I), B, d, F, k, nt))
+            if it:
+                times.append(time.perf_counter() - t0)
+        res[str(nt)] = round(1e3 * statistics.median(times), 3)
+    return {"config": "c0: fp32 B=32 d=768 F=16384 k=32", "op": "topk_sae_cpu (stk_cpu_forward)",
+            "median_ms_by_threads": res,
+            "rows_per_s_by_threads": {n: round(B / (ms * 1e-3), 1) for n, ms in res.items()},
+            "cpu_model": _cpu_model()}
+
+
 def copy_calibration(nbytes, steps):
     """Plain elementwise copy of `nbytes` fp32 bytes (torch's vectorised
     elementwise kernel: reads nbytes, writes nbytes), timed with HIP events.
@@ -265,6 +306,7 @@ def main():
     }
     if not args.no_cpu and wl["op"] == "exact":
         out["cpu_baseline"] = cpu_baseline(X, W, b, k, args.cpu_seconds)
+        out["cpu_c0"] = cpu_c0_baseline()
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)
