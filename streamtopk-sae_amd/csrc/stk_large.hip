@@ -5,14 +5,15 @@
 // form a 2 x 2 grid: each scores 128 latents x 128 rows per tile as 4 x 4
 // blocks of v_mfma_f32_32x32x16, with the 256 accumulators per lane in AGPRs.
 // Both operands come from LDS; each 16-byte operand read feeds 4 MFMAs.
-//   - W and X: whole 128-byte lines from global memory into registers, 2
-//     d-steps ahead, then into 2-stage LDS rings (W: 144-byte row stride; X:
-//     128-byte rows with the 16-byte chunks swizzled) that the MFMA-layout
-//     reads hit without bank conflicts.  One barrier per d-step.  The W lines
-//     are shared through L2 by the row blocks of the W range.
-//   - The next step's LDS stores and the loads two steps ahead are spread
-//     through the MFMA stream (one per MFMA), not issued as a burst: with
-//     one wave per SIMD, a blocked vector-memory issue stalls the MFMAs.
+//   - W and X: whole 128-byte lines loaded straight from global memory into
+//     2-stage LDS rings (buffer loads with the lds flag: no staging
+//     registers, no LDS-store instructions), one d-step ahead; 128-byte rows
+//     with the 16-byte chunks swizzled, so the MFMA-layout reads hit no bank
+//     conflicts.  One barrier per d-step.  The W lines are shared through L2
+//     by the row blocks of the W range.
+//   - The next step's LDS loads are spread through the first two quads'
+//     MFMAs (one per MFMA), not issued as a burst: with one wave per SIMD, a
+//     vector-memory instruction that cannot issue stalls the MFMAs behind it.
 //   - The pipeline restarts at every tile, so the epilogue holds no prefetch.
 //   - bias: the tile's 256 values are loaded at the tile start and staged in
 //     LDS for the epilogue.
@@ -45,7 +46,7 @@ constexpr int kLFrags = 4;                   // 32-latent fragments per wave
 constexpr int kLTile = 256;                  // latents per tile
 static_assert(2 * 32 * kLFrags == kLTile && 2 * 32 * kLNB == kLargeRows, "2 x 2 wave grid");
 constexpr int kLWChunks = kLTile * 8 / kLargeThreads;       // 16-byte W chunks per thread per d-step
-constexpr int kLWStage = kLTile * kXRowStride;              // W ring stage: 256 rows x 144 B (padded)
+constexpr int kLWStage = kLTile * kStepBytes;               // W ring stage: 256 rows x 128 B (swizzled)
 constexpr int kLXStage = kLargeRows * kStepBytes;           // X ring stage: 256 rows x 128 B (swizzled)
 constexpr int kLXChunks = kLargeRows * 8 / kLargeThreads;  // 16-byte X chunks per thread per d-step
 
@@ -57,7 +58,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_records, 0x00020000);
 }
 
-// X ring layout: row r's 16-byte chunk c sits in slot c ^ ((r >> 1) & 7) of the
+// LDS loads (global -> LDS, no registers): lane i of one instruction writes
+// the 16 bytes at ldsbase + 16*i.
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, unsigned char* ldsbase, int voff, int soff)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)ldsbase, 16, voff, soff, 0, 0);
+}
+
+// Ring layout: row r's 16-byte chunk c sits in slot c ^ ((r >> 1) & 7) of the
 // row's 128 bytes, so that the MFMA-layout reads (32 rows x one chunk per
 // half-wave) hit 16 distinct 16-byte bank groups.
 __device__ __forceinline__ int xswz(int r) { return (r >> 1) & 7; }
@@ -76,20 +84,22 @@ struct BigStream {
 
     // load cursors (absolute d-steps), uniform
     int ws, xs;
-    __amdgpu_buffer_rsrc_t wres[4], xres, zres;   // W: one resource per 64-row run of the tile
-    int wvoff[kLWChunks];        // W chunk p of this thread: offset within its run
-    int xvoff[kLXChunks];        // X chunk p of this thread: source offset within the row block
+    __amdgpu_buffer_rsrc_t wres, xres, zres;      // wres: this wave's 64-row run of the tile
+    int wvoff[kLWChunks];        // W LDS load i of this wave: this lane's source offset in the wave's run
+    int xvoff[kLXChunks];        // X LDS load i of this wave: this lane's source offset in the row block
     int xrd[4];                  // X operand read offset of quad q (row jl of block 0)
 
     __device__ __forceinline__ void init()
     {
-        // W chunk p: row (tid >> 3) + 32 p of the tile, 16-byte column tid & 7
+        // LDS load i of wave w fills rows 64 w + 8 i .. +7 of a stage (W: the
+        // wave's 64-row run of the tile; X: of the row block): lane -> row +
+        // lane / 8, slot lane % 8, which holds chunk slot ^ xswz(row)
 #pragma unroll
-        for (int p = 0; p < kLWChunks; ++p)
-            wvoff[p] = (((tid >> 3) + 32 * p) & 63) * (int)row_bytes + (tid & 7) * 16;
-        // X chunk p: row (tid >> 3) + 32 p of the row block, 16-byte column tid & 7
-#pragma unroll
-        for (int p = 0; p < kLXChunks; ++p) xvoff[p] = ((tid >> 3) + 32 * p) * (int)row_bytes + (tid & 7) * 16;
+        for (int i = 0; i < kLWChunks; ++i) {
+            const int r = 8 * i + (lane >> 3);   // row within the wave's 64
+            wvoff[i] = r * (int)row_bytes + (((lane & 7) ^ xswz(r)) * 16);
+            xvoff[i] = (wave * 64 + r) * (int)row_bytes + (((lane & 7) ^ xswz(r)) * 16);
+        }
 #pragma unroll
         for (int q = 0; q < 4; ++q) xrd[q] = jl * kStepBytes + (((h * 4 + q) ^ xswz(jl)) * 16);
         const int64_t nrows = (B - b0 < kLargeRows) ? B - b0 : kLargeRows;
@@ -101,58 +111,39 @@ struct BigStream {
     {
         ws = xs = s_lo;
         const int64_t tile0 = (tile_begin + t) * kLTile;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (SAMPLE) {
-                // each 64-row run is 64 consecutive latents of one sampled block
-                const int64_t f0 = sample_latent(tile0 + 64 * j, samp_log2);
-                wres[j] = make_rsrc(W + f0 * row_bytes, (int64_t)64 * row_bytes);
-            } else {
-                const int64_t f0 = tile0 + 64 * j;
-                int64_t n = F - f0;
-                n = n < 64 ? (n > 0 ? n : 0) : 64;
-                wres[j] = make_rsrc(W + (n > 0 ? f0 : 0) * row_bytes, n * row_bytes);
-            }
+        if (SAMPLE) {
+            // each 64-row run is 64 consecutive latents of one sampled block
+            const int64_t f0 = sample_latent(tile0 + 64 * wave, samp_log2);
+            wres = make_rsrc(W + f0 * row_bytes, (int64_t)64 * row_bytes);
+        } else {
+            const int64_t f0 = tile0 + 64 * wave;
+            int64_t n = F - f0;
+            n = n < 64 ? (n > 0 ? n : 0) : 64;
+            wres = make_rsrc(W + (n > 0 ? f0 : 0) * row_bytes, n * row_bytes);
         }
     }
 
-    // W of step ws (zeros past s_hi) into registers, whole 128-byte lines.
-    __device__ __forceinline__ void issue_w(u32x4 (&w)[kLWChunks])
+    // W of step ws (zeros past s_hi) straight into the W stage, whole 128-byte
+    // lines: this wave's 64-row run.
+    __device__ __forceinline__ void issue_w(unsigned char* wst)
     {
         const bool live = ws < s_hi;
+        const __amdgpu_buffer_rsrc_t r = live ? wres : zres;
         const int so = live ? ws * kStepBytes : 0;
 #pragma unroll
-        for (int p = 0; p < kLWChunks; ++p)
-            w[p] = __builtin_amdgcn_raw_buffer_load_b128(live ? wres[p >> 1] : zres, wvoff[p], so, 0);
+        for (int i = 0; i < kLWChunks; ++i) lds_load16(r, wst + (wave * 64 + 8 * i) * kStepBytes, wvoff[i], so);
         ++ws;
     }
 
-    __device__ __forceinline__ void store_w(const u32x4 (&w)[kLWChunks], unsigned char* wst) const
-    {
-#pragma unroll
-        for (int p = 0; p < kLWChunks; ++p)
-            *(u32x4*)(wst + ((tid >> 3) + 32 * p) * kXRowStride + (tid & 7) * 16) = w[p];
-    }
-
-    // X of step xs (zeros past s_hi and for rows past B) into registers, whole lines.
-    __device__ __forceinline__ void issue_x(u32x4 (&x)[kLXChunks])
+    // X of step xs (zeros past s_hi and for rows past B) straight into the X stage.
+    __device__ __forceinline__ void issue_x(unsigned char* xst)
     {
         const bool live = xs < s_hi;
         const __amdgpu_buffer_rsrc_t r = live ? xres : zres;
         const int so = live ? xs * kStepBytes : 0;
 #pragma unroll
-        for (int p = 0; p < kLXChunks; ++p) x[p] = __builtin_amdgcn_raw_buffer_load_b128(r, xvoff[p], so, 0);
+        for (int i = 0; i < kLXChunks; ++i) lds_load16(r, xst + (wave * 64 + 8 * i) * kStepBytes, xvoff[i], so);
         ++xs;
-    }
-
-    // Row r's chunk c goes to slot c ^ xswz(r) of the row's 128 bytes.
-    __device__ __forceinline__ void store_x(const u32x4 (&x)[kLXChunks], unsigned char* xst) const
-    {
-#pragma unroll
-        for (int p = 0; p < kLXChunks; ++p) {
-            const int r = (tid >> 3) + 32 * p;
-            *(u32x4*)(xst + r * kStepBytes + (((tid & 7) ^ xswz(r)) * 16)) = x[p];
-        }
     }
 
     // One d-step from LDS stages wst / xst, with the next step's staging folded
@@ -163,16 +154,15 @@ struct BigStream {
     // the background instead of stalling the wave's in-order issue.  Each quad
     // also reads the 8 operand blocks (4 W fragments, 4 X blocks) of the next.
     __device__ __forceinline__ void step(f32x16 (&acc)[kLFrags][kLNB], const unsigned char* wst,
-                                         const unsigned char* xst, u32x4 (&wr)[kLWChunks],
-                                         u32x4 (&xr)[kLXChunks], unsigned char* wnx, unsigned char* xnx)
+                                         const unsigned char* xst, unsigned char* wnx, unsigned char* xnx)
     {
-        const unsigned char* wl = wst + ((wave & 1) * (32 * kLFrags) + jl) * kXRowStride + h * 64;
+        const unsigned char* wl = wst + (wave & 1) * (32 * kLFrags) * kStepBytes;
         const unsigned char* xl = xst + (wave >> 1) * (32 * kLNB) * kStepBytes;
         u32x4 bA[kLNB], bB[kLNB], aA[kLFrags], aB[kLFrags];
 #pragma unroll
         for (int n = 0; n < kLNB; ++n) bA[n] = *(const u32x4*)(xl + xrd[0] + (32 * n) * kStepBytes);
 #pragma unroll
-        for (int fa = 0; fa < kLFrags; ++fa) aA[fa] = *(const u32x4*)(wl + (32 * fa) * kXRowStride);
+        for (int fa = 0; fa < kLFrags; ++fa) aA[fa] = *(const u32x4*)(wl + xrd[0] + (32 * fa) * kStepBytes);
         __builtin_amdgcn_sched_barrier(0);   // quad 0's operands are all in flight before any MFMA
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -183,7 +173,7 @@ struct BigStream {
             if (q < 3) {
 #pragma unroll
                 for (int fa = 0; fa < kLFrags; ++fa)
-                    wn[fa] = *(const u32x4*)(wl + (32 * fa) * kXRowStride + (q + 1) * 16);
+                    wn[fa] = *(const u32x4*)(wl + xrd[q + 1] + (32 * fa) * kStepBytes);
 #pragma unroll
                 for (int n = 0; n < kLNB; ++n) nxt[n] = *(const u32x4*)(xl + xrd[q + 1] + (32 * n) * kStepBytes);
             }
@@ -191,32 +181,26 @@ struct BigStream {
             for (int fa = 0; fa < kLFrags; ++fa)
 #pragma unroll
                 for (int n = 0; n < kLNB; ++n) mfma_quad<DT>(acc[fa][n], wc[fa], cur[n]);
-            if (q == 0) store_w(wr, wnx);
-            if (q == 1) store_x(xr, xnx);
-            if (q == 2) issue_w(wr);
-            if (q == 3) issue_x(xr);
-            // (MFMA, DS read) x 8 then (MFMA, staging op) x 8; quad 3: (MFMA, VMEM) x 8, MFMA x 8
+            if (q == 0) issue_w(wnx);
+            if (q == 1) issue_x(xnx);
+            // (MFMA, DS read) x 8, then quads 0 and 1: (MFMA, LDS load) x 8; others: MFMA x 8
             if (q < 3) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
                 }
+            }
+            if (q < 2) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    if (q < 2)
-                        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // DS write
-                    else
-                        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM read
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM read (to LDS)
                 }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-                }
+            } else if (q < 3) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+            } else {
+                __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -323,8 +307,6 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
 
     if (bs.ntiles > 0) {
         bs.init();
-        u32x4 wA[kLWChunks], wB[kLWChunks];
-        u32x4 xA[kLXChunks], xB[kLXChunks];
 
         f32x16 acc[kLFrags][kLNB];
 #pragma unroll
@@ -343,24 +325,22 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                 const int64_t f = tile0 + tid;
                 bnext = a.bias[f < F ? f : F - 1];
             }
-            // Per d-step: W and X two steps ahead in registers, then 2-stage LDS
-            // rings (W padded, X swizzled); one barrier per d-step.  Loads past
-            // the last step read zeros.
+            // Per d-step: W and X one step ahead, loaded straight into 2-stage
+            // LDS rings (128-byte rows, 16-byte chunks swizzled) during the
+            // first two quads of the step before; one barrier per d-step, after
+            // the wave's own loads of the next step have landed.  Loads past the
+            // last step read zeros.
             bs.begin_tile(t);
-            bs.issue_w(wA);   // W(0)
-            bs.issue_x(xA);   // X(0)
-            bs.issue_w(wB);   // W(1)
-            bs.issue_x(xB);   // X(1)
-            bs.store_w(wA, wst0);
-            bs.store_x(xA, xs0);
-            bs.issue_w(wA);   // W(2)
-            bs.issue_x(xA);   // X(2)
+            bs.issue_w(wst0);   // W(0)
+            bs.issue_x(xs0);    // X(0)
             // a padded last step (s >= nds) reads zeros: every step computes unconditionally
             for (int s = 0; s < bs.nds2; s += 2) {
-                __syncthreads();   // step s in stage 0; stage 1 was last read in step s-1
-                bs.step(acc, wst0, xs0, wB, xB, wst1, xs1);   // stages W/X(s+1), loads W/X(s+3)
-                __syncthreads();
-                bs.step(acc, wst1, xs1, wA, xA, wst0, xs0);   // stages W/X(s+2), loads W/X(s+4)
+                __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0): W/X(s) in stage 0
+                __builtin_amdgcn_s_barrier();         // ... for every wave; stage 1 free
+                bs.step(acc, wst0, xs0, wst1, xs1);   // loads W/X(s+1) into stage 1
+                __builtin_amdgcn_s_waitcnt(0x0070);
+                __builtin_amdgcn_s_barrier();
+                bs.step(acc, wst1, xs1, wst0, xs0);   // loads W/X(s+2) into stage 0
             }
             // the loads past the last step (zeros) land before the rings are reused
             __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0)
