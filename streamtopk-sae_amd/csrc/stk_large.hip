@@ -146,13 +146,12 @@ struct BigStream {
         ++xs;
     }
 
-    // One d-step from LDS stages wst / xst, with the next step's staging folded
-    // into the MFMA stream: W(s+1) and X(s+1) go from registers into the other
-    // stages (wnx / xnx) during quads 0 and 1, and their registers are reloaded
-    // with W(s+3) / X(s+3) during quads 2 and 3.  One vector-memory or LDS-write
-    // instruction sits between MFMAs, so the texture path and the LDS work in
-    // the background instead of stalling the wave's in-order issue.  Each quad
-    // also reads the 8 operand blocks (4 W fragments, 4 X blocks) of the next.
+    // One d-step from LDS stages wst / xst, with the next step's LDS loads
+    // folded into the MFMA stream: W(s+1) into wnx during quad 0 and X(s+1)
+    // into xnx during quad 1, one load instruction between MFMAs, so that the
+    // texture path works in the background instead of stalling the wave's
+    // in-order issue.  Each quad also reads the 8 operand blocks (4 W
+    // fragments, 4 X blocks) of the next.
     __device__ __forceinline__ void step(f32x16 (&acc)[kLFrags][kLNB], const unsigned char* wst,
                                          const unsigned char* xst, unsigned char* wnx, unsigned char* xnx)
     {
@@ -240,7 +239,11 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
     uint64_t* cscr = (uint64_t*)(qrow + kLargeRows);                  // [waves][cap]
     const int cap = a.cap, k = a.k;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // wave is read into a scalar register so that the compiler knows it is
+    // uniform: the per-wave buffer resources then stay in scalar registers
+    // (a resource the compiler takes for divergent costs a waterfall loop
+    // around every load).
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, jl = lane & 31;
     const int lw0 = (wave & 1) * (32 * kLFrags);   // this wave's first latent of the tile
     const int rw0 = (wave >> 1) * (32 * kLNB);     // this wave's first row of the row block
