@@ -234,7 +234,7 @@ __device__ __forceinline__ void compact_full_rows(int* cnt, uint64_t* thr, uint6
         const int i = __builtin_ctzll(full);
         full &= full - 1;
         const int row = wave * R + i;
-        uint64_t* q = qrow(row);
+        auto* q = qrow(row);
         uint64_t e[3];
 #pragma unroll
         for (int m = 0; m < 3; ++m) {

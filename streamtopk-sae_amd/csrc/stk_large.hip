@@ -53,9 +53,17 @@ constexpr int kLXChunks = kLargeRows * 8 / kLargeThreads;  // 16-byte X chunks p
 // Buffer resource (raw, gfx9 family): loads at byte offsets >= num_records
 // return zeros, which bounds rows past B and latents past F, and a zero-length
 // resource makes whole steps read as zeros.
+// Every resource of this file is uniform over the wave; its fields go through
+// readfirstlane so that the compiler keeps it in scalar registers whatever
+// its uniformity analysis concludes (a resource it takes for divergent costs
+// a waterfall loop around every load).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t num_records)
 {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_records, 0x00020000);
+    const uint64_t b = (uint64_t)base;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    const int n = __builtin_amdgcn_readfirstlane((int)num_records);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, n, 0x00020000);
 }
 
 // LDS loads (global -> LDS, no registers): lane i of one instruction writes
@@ -69,6 +77,19 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, unsigned ch
 // row's 128 bytes, so that the MFMA-layout reads (32 rows x one chunk per
 // half-wave) hit 16 distinct 16-byte bank groups.
 __device__ __forceinline__ int xswz(int r) { return (r >> 1) & 7; }
+
+typedef __attribute__((address_space(1))) uint64_t gu64;   // a key in global memory
+
+// Calls f(std::integral_constant<int, i>) for i = 0 .. N-1 (compile-time i, so
+// that accumulator indices stay static).
+template <int N, int I = 0, class Fn>
+__device__ __forceinline__ void static_for(Fn&& f)
+{
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, I + 1>(f);
+    }
+}
 
 template <int DT, bool SAMPLE>
 struct BigStream {
@@ -127,9 +148,10 @@ struct BigStream {
     // lines: this wave's 64-row run.
     __device__ __forceinline__ void issue_w(unsigned char* wst)
     {
-        const bool live = ws < s_hi;
+        const int w = __builtin_amdgcn_readfirstlane(ws);
+        const bool live = w < s_hi;
         const __amdgpu_buffer_rsrc_t r = live ? wres : zres;
-        const int so = live ? ws * kStepBytes : 0;
+        const int so = live ? w * kStepBytes : 0;
 #pragma unroll
         for (int i = 0; i < kLWChunks; ++i) lds_load16(r, wst + (wave * 64 + 8 * i) * kStepBytes, wvoff[i], so);
         ++ws;
@@ -138,9 +160,10 @@ struct BigStream {
     // X of step xs (zeros past s_hi and for rows past B) straight into the X stage.
     __device__ __forceinline__ void issue_x(unsigned char* xst)
     {
-        const bool live = xs < s_hi;
+        const int x = __builtin_amdgcn_readfirstlane(xs);
+        const bool live = x < s_hi;
         const __amdgpu_buffer_rsrc_t r = live ? xres : zres;
-        const int so = live ? xs * kStepBytes : 0;
+        const int so = live ? x * kStepBytes : 0;
 #pragma unroll
         for (int i = 0; i < kLXChunks; ++i) lds_load16(r, xst + (wave * 64 + 8 * i) * kStepBytes, xvoff[i], so);
         ++xs;
@@ -206,6 +229,15 @@ struct BigStream {
     }
 };
 
+// m * 2 + !(v < tv): one bit of a score mask, shifted in from the top
+// (v_cmp into VCC, then the add takes VCC as its carry-in).
+__device__ __forceinline__ uint32_t mask_step(uint32_t m, float v, float tv)
+{
+    uint32_t r;
+    asm("v_cmp_nlt_f32 vcc, %1, %2\n\tv_addc_co_u32 %0, vcc, %3, %3, vcc" : "=v"(r) : "v"(v), "v"(tv), "v"(m) : "vcc");
+    return r;
+}
+
 // An accumulator element read into a VGPR at the point of use.  Volatile, so
 // the compiler cannot keep VGPR copies of all 256 accumulators alive across
 // the epilogue's passes (which spills).
@@ -235,7 +267,10 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
     float* bias_s = (float*)(xs1 + kLXStage);                         // [kLTile]
     uint64_t* thr = (uint64_t*)(bias_s + kLTile);                    // [rows]
     int* cnt = (int*)(thr + kLargeRows);                              // [rows]
-    uint64_t** qrow = (uint64_t**)(cnt + kLargeRows);                 // [rows] segment of each row
+    // [rows] segment of each row.  Typed as global pointers: read back from LDS,
+    // a plain pointer would make every segment access a flat instruction, which
+    // the LDS waits (lgkmcnt) of the survivor walk would then wait for.
+    gu64** qrow = (gu64**)(cnt + kLargeRows);
     uint64_t* cscr = (uint64_t*)(qrow + kLargeRows);                  // [waves][cap]
     const int cap = a.cap, k = a.k;
 
@@ -275,7 +310,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
             const int64_t row = b0 + i;
             cnt[i] = 0;
             thr[i] = (row < B) ? a.thr0[row] : 0ull;
-            qrow[i] = a.list_keys + ((row < B) ? row : 0) * a.list_cap + a.head_span + (int64_t)rg * cap;
+            qrow[i] = (gu64*)(a.list_keys + ((row < B) ? row : 0) * a.list_cap + a.head_span + (int64_t)rg * cap);
         }
     }
 
@@ -373,12 +408,14 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
             __syncthreads();
 
             // ---- epilogue: bias, threshold filter, append to the row segments ----
-            // One row block at a time.  Its 64 scores per lane are read from the
-            // accumulators once, in straight-line code, biased and compared with
-            // the row threshold; they go to this wave's LDS staging area ([bit]
-            // [lane], in the idle W ring), where the survivor walk and any
-            // recheck read them back.  Bit 16*fa + r of a row mask is latent
-            // lat0 + fa*32 + 8*(r/4) + r%4; this lane's row is rw0 + 32*n + jl.
+            // One row block at a time, with no barrier between blocks.  Its 64
+            // scores per lane are read from the accumulators once, in
+            // straight-line code, biased and compared with the row threshold;
+            // they go to this wave's LDS staging area ([bit][lane], in the idle W
+            // ring), where the survivor walk reads them back.  Bit 16*fa + r of a
+            // row mask is latent lat0 + fa*32 + 8*(r/4) + r%4; this lane's row is
+            // rw0 + 32*n + jl.  Survivors that find their row segment full are
+            // kept in ovf[n] and handled after one barrier for the whole tile.
             const bool edge = tile0 + kLTile > F ||
                               (a.sampled && (is_sampled(tile0, a.samp_log2, a.samp_blocks) ||
                                              is_sampled(tile0 + kLTile - 1, a.samp_log2, a.samp_blocks)));
@@ -395,68 +432,120 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                     vmask |= ok ? (1ull << bit) : 0ull;
                 }
             }
+            // This wave's staging area: [lane][64 scores]; 16-byte chunk c of a
+            // lane's 256 bytes sits in slot c ^ (lane & 15), so that the b128
+            // writes of 16 consecutive lanes hit distinct banks.
             float* stage = (float*)wst0 + wave * (16 * kLFrags * 64);
+            // This wave's survivor descriptors (the X ring is idle): up to 64 per lane.
+            uint32_t* dlist = (uint32_t*)xs0 + wave * (64 * 64);
+            auto stage_at = [&](int ln, int bit) -> float {
+                return stage[ln * 64 + ((((bit >> 2) ^ (ln & 15))) << 2) + (bit & 3)];
+            };
+            // Stages row block n's biased scores; returns the mask of those not
+            // below threshold tv.
+            // this lane's 64 bias values, in registers for all row blocks
+            f32x4 bias_r[kLFrags * 4];
 #pragma unroll
-            for (int n = 0; n < kLNB; ++n) {
+            for (int i = 0; i < kLFrags * 4; ++i) bias_r[i] = *(const f32x4*)(bias_l + (i >> 2) * 32 + 8 * (i & 3));
+            auto stage_block = [&](auto nc, float tv) -> uint64_t {
+                constexpr int n = decltype(nc)::value;
+                uint64_t msk = 0;
+#pragma unroll
+                for (int fa = 0; fa < kLFrags; ++fa) {
+                    uint32_t m = 0;
+#pragma unroll
+                    for (int r4 = 3; r4 >= 0; --r4) {
+                        const f32x4 bv = bias_r[fa * 4 + r4];
+                        f32x4 v;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = agpr_read(acc[fa][n][4 * r4 + e]) + bv[e];
+                        *(f32x4*)(stage + lane * 64 + (((4 * fa + r4) ^ (lane & 15)) << 2)) = v;
+#pragma unroll
+                        for (int e = 3; e >= 0; --e) m = mask_step(m, v[e], tv);   // bits 15 .. 0
+                    }
+                    msk |= (uint64_t)m << (16 * fa);
+                }
+                return msk;
+            };
+            // Appends the staged scores of the bits of pend (row block n) to the
+            // rows' segments; returns the bits that found their segment full.
+            // The lanes' survivors are spread over the whole wave: each lane
+            // lists its own as descriptors (slot, bit, lane) at its offset in the
+            // wave's list, then every lane stores one listed survivor per round.
+            auto append = [&](auto nc, uint64_t pend) -> uint64_t {
+                constexpr int n = decltype(nc)::value;
                 const int row = rw0 + 32 * n + jl;
-                uint64_t pend = 0;
-                {
-                    const uint64_t tk = thr[row];
-                    const float tv = tk ? key_value(tk) : -__builtin_inff();
+                const int c = __popcll(pend);
+                const int base = c ? atomicAdd(&cnt[row], c) : 0;
+                __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+                int nfit = cap - base;
+                nfit = nfit < 0 ? 0 : (nfit > c ? c : nfit);
+                // exclusive prefix sum of nfit (<= 64) over the wave, from its bit planes
+                int off = 0, total = 0;
 #pragma unroll
-                    for (int fa = 0; fa < kLFrags; ++fa) {
-                        const f32x4 b0v = *(const f32x4*)(bias_l + fa * 32);
-                        const f32x4 b1v = *(const f32x4*)(bias_l + fa * 32 + 8);
-                        const f32x4 b2v = *(const f32x4*)(bias_l + fa * 32 + 16);
-                        const f32x4 b3v = *(const f32x4*)(bias_l + fa * 32 + 24);
-                        uint32_t m = 0;
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const f32x4 bv = (r < 4) ? b0v : (r < 8) ? b1v : (r < 12) ? b2v : b3v;
-                            const float v = agpr_read(acc[fa][n][r]) + bv[r & 3];
-                            stage[(fa * 16 + r) * 64 + lane] = v;
-                            m |= (!(v < tv)) ? (1u << r) : 0u;
-                        }
-                        pend |= (uint64_t)m << (16 * fa);
-                    }
+                for (int bp = 0; bp < 7; ++bp) {
+                    const uint64_t bal = __ballot((nfit >> bp) & 1);
+                    off += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                          __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u)) << bp;
+                    total += __popcll(bal) << bp;
                 }
+                uint64_t mm = pend;
+                for (int i = 0; i < nfit; ++i) {
+                    const int bit = __builtin_ctzll(mm);
+                    mm &= mm - 1u;
+                    dlist[off + i] = ((uint32_t)(base + i) << 12) | ((uint32_t)bit << 6) | (uint32_t)lane;
+                }
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                for (int j = lane; j < total; j += 64) {
+                    const uint32_t dsc = dlist[j];
+                    const int ln = dsc & 63, bit = (dsc >> 6) & 63, slot = (int)(dsc >> 12);
+                    const int lat = (int)tile0 + lw0 + (ln >> 5) * 4 + (bit >> 4) * 32 + ((bit & 15) >> 2) * 8 + (bit & 3);
+                    qrow[rw0 + 32 * n + (ln & 31)][slot] = make_key(stage_at(ln, bit), lat);
+                }
+                __builtin_amdgcn_wave_barrier();
+                return mm;
+            };
+            uint64_t ovf[kLNB];
+            static_for<kLNB>([&](auto nc) {
+                constexpr int n = decltype(nc)::value;
+                const int row = rw0 + 32 * n + jl;
+                const uint64_t tk = thr[row];
+                uint64_t pend = stage_block(nc, tk ? key_value(tk) : -__builtin_inff());
                 pend = (b0 + row < B) ? (pend & vmask) : 0ull;
-                uint64_t* q = qrow[row];
-                for (int it = 0; it < 1 << 20; ++it) {
-                    const int base = pend ? atomicAdd(&cnt[row], __popcll(pend)) : 0;
-                    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
-                    // each lane walks only its own set bits and reads each score back by address
-                    uint64_t keep = 0, mm = pend;
-                    int slot = base;
-                    while (mm) {
-                        const int bit = __builtin_ctzll(mm);
-                        mm &= mm - 1u;
-                        if (slot < cap) {
+                ovf[n] = append(nc, pend);
+            });
+            if (__syncthreads_or((ovf[0] | ovf[1] | ovf[2] | ovf[3]) != 0)) {
+                // Rare: some row segments are full.  Block by block: compact the
+                // full segments to their top k (which raises their thresholds),
+                // drop the pending scores now below threshold, append the rest;
+                // repeat until nothing is pending.
+                static_for<kLNB>([&](auto nc) {
+                    constexpr int n = decltype(nc)::value;
+                    const int row = rw0 + 32 * n + jl;
+                    uint64_t pend = ovf[n];
+                    if (!__syncthreads_or(pend != 0)) return;
+                    stage_block(nc, 0.f);   // this block's scores back into the staging area
+                    for (int it = 0; it < 1 << 20; ++it) {
+                        __threadfence_block();   // this thread's segment stores are complete
+                        __syncthreads();
+                        compact_full_rows<kLargeRows / kLWaves>(cnt, thr, cscr + wave * cap,
+                                                               [&](int r) { return qrow[r]; }, cap, k, wave, lane);
+                        __threadfence_block();
+                        __syncthreads();
+                        // drop pending scores that fell below the raised threshold
+                        const uint64_t tk = thr[row];
+                        uint64_t mm2 = pend;
+                        while (mm2) {
+                            const int bit = __builtin_ctzll(mm2);
+                            mm2 &= mm2 - 1u;
                             const int off = (bit >> 4) * 32 + ((bit & 15) >> 2) * 8 + (bit & 3);
-                            q[slot] = make_key(stage[bit * 64 + lane], lat0 + off);
-                        } else {
-                            keep |= 1ull << bit;
+                            if (!(make_key(stage_at(lane, bit), lat0 + off) > tk)) pend &= ~(1ull << bit);
                         }
-                        ++slot;
+                        pend = append(nc, pend);
+                        if (!__syncthreads_or(pend != 0)) break;
                     }
-                    pend = keep;
-                    if (!__syncthreads_or(keep != 0)) break;
-                    __threadfence_block();   // this thread's segment stores are complete
-                    __syncthreads();
-                    compact_full_rows<kLargeRows / kLWaves>(cnt, thr, cscr + wave * cap,
-                                                           [&](int r) { return qrow[r]; }, cap, k, wave, lane);
-                    __threadfence_block();
-                    __syncthreads();
-                    // drop pending scores that fell below the raised threshold
-                    const uint64_t tk = thr[row];
-                    uint64_t mm2 = pend;
-                    while (mm2) {
-                        const int bit = __builtin_ctzll(mm2);
-                        mm2 &= mm2 - 1u;
-                        const int off = (bit >> 4) * 32 + ((bit & 15) >> 2) * 8 + (bit & 3);
-                        if (!(make_key(stage[bit * 64 + lane], lat0 + off) > tk)) pend &= ~(1ull << bit);
-                    }
-                }
+                });
             }
 #pragma unroll
             for (int fa = 0; fa < kLFrags; ++fa)
