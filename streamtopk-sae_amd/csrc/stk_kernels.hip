@@ -476,6 +476,7 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
 {
     __shared__ SelShared S;
     __shared__ int scnt[kMergeMaxSeg];
+    __shared__ int spre[kMergeMaxSeg];   // inclusive prefix sums of scnt
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
     const int k = a.k;
@@ -489,27 +490,73 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
         v[u] = keys[i < a.list_cap ? i : a.list_cap - 1];
     }
     for (int sg = tid; sg < nseg; sg += kThreads) scnt[sg] = a.seg_cnt[row * nseg + sg];
-    const int64_t n = nseg ? a.head_span + (int64_t)nseg * a.seg_cap : hc;
     if (tid == 0) S.cnt = 0;
     __syncthreads();
+    // Candidate i (0 <= i < n) is head key i for i < hc, else key i - hc of
+    // the segments' valid keys taken in order: the chunks run over valid keys
+    // only, however full the segments are.
+    int64_t n = hc;
+    int top = 0;   // largest power of two <= nseg
+    if (nseg > 0) {
+        if (tid < 64) {
+            int carry = 0;
+            for (int s0 = 0; s0 < nseg; s0 += 64) {
+                int c = s0 + tid < nseg ? scnt[s0 + tid] : 0;
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) {
+                    const int t = __shfl_up(c, o);
+                    if (tid >= o) c += t;
+                }
+                if (s0 + tid < nseg) spre[s0 + tid] = carry + c;
+                carry += __shfl(c, 63);
+            }
+        }
+        __syncthreads();
+        n = hc + spre[nseg - 1];
+        top = 1 << (31 - __builtin_clz(nseg));
+    }
     uint64_t run = 0;
     for (int64_t c0 = 0; c0 < n; c0 += (int64_t)kPer * kThreads) {
         uint64_t m = 0;
+        if (nseg > 0) {
+            // segment of each segment candidate: the number of segments whose
+            // inclusive prefix is <= its index (all items searched in step)
+            int j[kPer], pos[kPer];
 #pragma unroll
-        for (int u = 0; u < kPer; ++u) {
-            const int64_t i = c0 + tid + (int64_t)u * kThreads;
-            bool ok = i < n;
-            if (ok && i >= a.head_span) {
-                const int jj = (int)(i - a.head_span);
-                const int sg = jj / a.seg_cap;
-                ok = jj - sg * a.seg_cap < scnt[sg];
-            } else if (ok) {
-                ok = i < hc;
+            for (int u = 0; u < kPer; ++u) {
+                j[u] = (int)(c0 + tid + (int64_t)u * kThreads - hc);
+                pos[u] = 0;
             }
-            if (u < kSpec && c0 == 0)
-                v[u] = ok ? v[u] : 0ull;
-            else
-                v[u] = ok ? keys[i] : 0ull;
+            for (int st = top; st > 0; st >>= 1) {
+#pragma unroll
+                for (int u = 0; u < kPer; ++u) {
+                    const int q = pos[u] + st - 1;
+                    if (q < nseg && spre[q] <= j[u]) pos[u] += st;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kPer; ++u) {
+                const int64_t i = c0 + tid + (int64_t)u * kThreads;
+                if (i >= n) {
+                    v[u] = 0ull;
+                } else if (i < hc) {
+                    v[u] = keys[i];
+                } else {
+                    const int sg = pos[u];
+                    const int off = j[u] - (spre[sg] - scnt[sg]);
+                    v[u] = keys[a.head_span + (int64_t)sg * a.seg_cap + off];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < kPer; ++u) {
+                const int64_t i = c0 + tid + (int64_t)u * kThreads;
+                const bool ok = i < n;
+                if (u < kSpec && c0 == 0)
+                    v[u] = ok ? v[u] : 0ull;
+                else
+                    v[u] = ok ? keys[i] : 0ull;
+            }
         }
 #pragma unroll
         for (int u = 0; u < kPer; ++u) m = v[u] > m ? v[u] : m;
