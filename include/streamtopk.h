@@ -64,6 +64,31 @@ int stk_exact_forward(const void* X, const void* W, const float* b, float* V, in
                       int64_t B, int64_t d, int64_t F, int64_t k, int dtype,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* Exact encode of one shard of W: W and b hold latents f_offset ..
+ * f_offset + F - 1 of a larger dictionary, and I receives those global
+ * indices (local index + f_offset).  Otherwise identical to
+ * stk_exact_forward, with the same workspace (stk_exact_workspace_bytes for
+ * the shard's F).  No counterpart in the reference, which runs one device
+ * (device 0's attributes, streamtopk_exact.cu:658): it is the per-GPU part of
+ * an F-sharded encoder, whose per-shard results stk_topk_merge combines.
+ * Requires 0 <= f_offset and f_offset + F <= 2^31 - 1. */
+int stk_exact_forward_shard(const void* X, const void* W, const float* b, float* V, int32_t* I,
+                            int64_t B, int64_t d, int64_t F, int64_t k, int dtype, int64_t f_offset,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* Device workspace (bytes) for stk_topk_merge. */
+int stk_topk_merge_workspace_bytes(int64_t B, int64_t k, int64_t nparts, size_t* out_bytes);
+
+/* Top-k of nparts partial top-k results: Vp / Ip are (nparts, B, k) fp32
+ * values and int32 global indices, e.g. the stk_exact_forward_shard outputs
+ * of W's shards gathered on one device; V / I receive each row's top k of
+ * the nparts * k candidates, in the library's order (value descending, then
+ * lower index first).  No counterpart in the reference (see
+ * stk_exact_forward_shard).  k as for stk_exact_forward; nparts >= 1 and
+ * nparts * k <= 2^20. */
+int stk_topk_merge(const float* Vp, const int32_t* Ip, int64_t nparts, int64_t B, int64_t k,
+                   float* V, int32_t* I, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Device workspace (bytes) for stk_approx_forward.  `with_candidates` is
  * non-zero when the caller passes a candidate buffer. */
 int stk_approx_workspace_bytes(int64_t B, int64_t d, int64_t F, int64_t k, int64_t c, int dtype,

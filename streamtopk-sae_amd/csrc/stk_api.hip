@@ -267,7 +267,8 @@ static int validate_exact(int64_t B, int64_t d, int64_t F, int64_t k, int dtype)
 
 // Runs sample -> thr -> main -> merge on `st`.
 static int run_exact(const ExactPlan& p, const void* X, const void* W, const float* b, float* V, int32_t* I,
-                     int64_t B, int64_t d, int64_t F, int64_t k, int dtype, unsigned char* ws, hipStream_t st)
+                     int64_t B, int64_t d, int64_t F, int64_t k, int dtype, unsigned char* ws, hipStream_t st,
+                     int64_t f_offset = 0)
 {
     const int dt = dtype;   // STK_DTYPE_* and DT_* share values
     hipError_t e;
@@ -357,6 +358,7 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         mg.spec = (p.sample && k + k * F / p.nsamp > 4096) ? 1 : 0;
     }
     mg.k = (int)k;
+    mg.f_offset = (int32_t)f_offset;
     mg.V = V; mg.I = I;
     const int pg = prof_begin("merge_kernel", st);
     e = launch_merge(mg, B, st);
@@ -443,6 +445,98 @@ int stk_exact_forward(const void* X, const void* W, const float* b, float* V, in
                          workspace ? workspace_bytes : (size_t)0, p.total);
     if ((uintptr_t)workspace & 255) return set_error(STK_E_INVALID, "workspace must be 256-byte aligned");
     return run_exact(p, X, W, b, V, I, B, d, F, k, dtype, (unsigned char*)workspace, (hipStream_t)stream);
+}
+
+int stk_exact_forward_shard(const void* X, const void* W, const float* b, float* V, int32_t* I,
+                            int64_t B, int64_t d, int64_t F, int64_t k, int dtype, int64_t f_offset,
+                            void* workspace, size_t workspace_bytes, void* stream)
+{
+    clear_error();
+    if (f_offset < 0 || f_offset > 0x7FFFFFFELL)
+        return set_error(STK_E_INVALID, "f_offset=%lld out of range", (long long)f_offset);
+    int rc = validate_exact(B, d, F, k, dtype);
+    if (rc) return rc;
+    if (f_offset + F > 0x7FFFFFFFLL)
+        return set_error(STK_E_INVALID, "f_offset + F = %lld exceeds the int32 index range",
+                         (long long)(f_offset + F));
+    if (B == 0) return 0;
+    if ((rc = check_ptrs(X, W, b, V, I))) return rc;
+    int ncu = 0;
+    if ((rc = cu_count(&ncu))) return rc;
+    const ExactPlan p = make_exact_plan(B, d, F, k, dtype, ncu);
+    if (!workspace || workspace_bytes < p.total)
+        return set_error(STK_E_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required",
+                         workspace ? workspace_bytes : (size_t)0, p.total);
+    if ((uintptr_t)workspace & 255) return set_error(STK_E_INVALID, "workspace must be 256-byte aligned");
+    return run_exact(p, X, W, b, V, I, B, d, F, k, dtype, (unsigned char*)workspace, (hipStream_t)stream,
+                     f_offset);
+}
+
+// Merge workspace: the dense candidate lists (nparts*k keys per row) and the
+// per-row counts.
+static int validate_merge(int64_t B, int64_t k, int64_t nparts)
+{
+    if (B < 0) return set_error(STK_E_INVALID, "invalid shape: B=%lld", (long long)B);
+    if (k < 1 || !k_supported(k))
+        return set_error(STK_E_INVALID, "unsupported k=%lld. Supported: 1,2,4,8,16,32,64,128.", (long long)k);
+    if (nparts < 1 || nparts * k > (1 << 20))
+        return set_error(STK_E_INVALID, "nparts=%lld out of range (1 <= nparts, nparts * k <= 2^20)",
+                         (long long)nparts);
+    return 0;
+}
+
+static size_t merge_ws_lcnt(int64_t B, int64_t k, int64_t nparts)
+{
+    return ((size_t)B * (size_t)(nparts * k) * 8 + 255) & ~(size_t)255;
+}
+
+int stk_topk_merge_workspace_bytes(int64_t B, int64_t k, int64_t nparts, size_t* out_bytes)
+{
+    clear_error();
+    if (!out_bytes) return set_error(STK_E_INVALID, "null out_bytes");
+    int rc = validate_merge(B, k, nparts);
+    if (rc) return rc;
+    *out_bytes = (B == 0) ? 0 : merge_ws_lcnt(B, k, nparts) + (size_t)B * kCntStride * 4;
+    return 0;
+}
+
+int stk_topk_merge(const float* Vp, const int32_t* Ip, int64_t nparts, int64_t B, int64_t k,
+                   float* V, int32_t* I, void* workspace, size_t workspace_bytes, void* stream)
+{
+    clear_error();
+    int rc = validate_merge(B, k, nparts);
+    if (rc) return rc;
+    if (B == 0) return 0;
+    if (!Vp || !Ip || !V || !I) return set_error(STK_E_INVALID, "null tensor pointer");
+    if (((uintptr_t)Vp | (uintptr_t)Ip | (uintptr_t)V | (uintptr_t)I) & 3)
+        return set_error(STK_E_INVALID, "values and indices must be 4-byte aligned");
+    const size_t need = merge_ws_lcnt(B, k, nparts) + (size_t)B * kCntStride * 4;
+    if (!workspace || workspace_bytes < need)
+        return set_error(STK_E_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required",
+                         workspace ? workspace_bytes : (size_t)0, need);
+    if ((uintptr_t)workspace & 255) return set_error(STK_E_INVALID, "workspace must be 256-byte aligned");
+    unsigned char* ws = (unsigned char*)workspace;
+    const hipStream_t st = (hipStream_t)stream;
+    PackArgs pa;
+    pa.V = Vp; pa.I = Ip; pa.B = B; pa.k = (int)k; pa.nparts = (int)nparts;
+    pa.list_keys = (uint64_t*)ws;
+    pa.list_cnt = (int32_t*)(ws + merge_ws_lcnt(B, k, nparts));
+    pa.list_cap = nparts * k;
+    hipError_t e = launch_pack(pa, B, st);
+    if (e != hipSuccess) return hip_fail(e, "pack_kernel launch");
+    MergeArgs mg;
+    std::memset(&mg, 0, sizeof mg);
+    mg.list_keys = pa.list_keys; mg.list_cnt = pa.list_cnt; mg.list_cap = pa.list_cap;
+    mg.head_span = pa.list_cap; mg.nseg = 0; mg.seg_cap = 1; mg.seg_cnt = nullptr;
+    mg.spec = nparts * k > 4096 ? 1 : 0;
+    mg.k = (int)k;
+    mg.f_offset = 0;
+    mg.V = V; mg.I = I;
+    const int pg = prof_begin("merge_kernel", st);
+    e = launch_merge(mg, B, st);
+    prof_end(pg, st);
+    if (e != hipSuccess) return hip_fail(e, "merge_kernel launch");
+    return 0;
 }
 
 int stk_approx_workspace_bytes(int64_t B, int64_t d, int64_t F, int64_t k, int64_t c, int dtype,

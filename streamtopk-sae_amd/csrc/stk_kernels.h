@@ -142,8 +142,19 @@ struct MergeArgs {
     int k;
     int spec;                    // non-zero: a dense list expected to hold more than
                                  //   4096 candidates (one-chunk variant)
+    int32_t f_offset;            // added to every emitted index (a shard's first latent)
     float* V;
     int32_t* I;
+};
+
+struct PackArgs {                // partial top-k results -> dense candidate lists
+    const float* V;              // [nparts][B][k]
+    const int32_t* I;            // [nparts][B][k] latent indices
+    int64_t B;
+    int k, nparts;
+    uint64_t* list_keys;         // [B][list_cap]
+    int32_t* list_cnt;           // [B * kCntStride]
+    int64_t list_cap;
 };
 
 struct GroupArgs {               // approximate variant, per-group top-c candidates
@@ -177,6 +188,7 @@ hipError_t launch_mainl_sample(int dt, const MainLArgs& a, int grid, hipStream_t
 hipError_t launch_sample(int dt, int NB, const SampleArgs& a, dim3 grid, hipStream_t st);
 hipError_t launch_thr(const ThrArgs& a, int64_t rows, hipStream_t st);
 hipError_t launch_merge(const MergeArgs& a, int64_t rows, hipStream_t st);
+hipError_t launch_pack(const PackArgs& a, int64_t rows, hipStream_t st);
 hipError_t launch_group(int dt, int NB, const GroupArgs& a, dim3 grid, hipStream_t st);
 hipError_t launch_cand(const CandArgs& a, int64_t rows, hipStream_t st);
 hipError_t launch_read_probe(const void* buf, int64_t n16, uint32_t* sink, int ncu, hipStream_t st);

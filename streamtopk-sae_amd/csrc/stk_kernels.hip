@@ -591,8 +591,26 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
     }
     emit_topk(S, k, tid, [&](int r, uint64_t kk) {
         a.V[row * k + r] = key_value(kk);
-        a.I[row * k + r] = key_index(kk);
+        a.I[row * k + r] = key_index(kk) + a.f_offset;
     });
+}
+
+// ---------------------------------------------------------------------------
+// pack_kernel: the rows of nparts partial (B, k) results (values and global
+// latent indices, e.g. one per W shard) as keys of a dense candidate list per
+// row, for merge_kernel.  One workgroup per row.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void pack_kernel(PackArgs a)
+{
+    const int64_t row = blockIdx.x;
+    const int n = a.nparts * a.k;
+    uint64_t* out = a.list_keys + row * a.list_cap;
+    for (int j = threadIdx.x; j < n; j += kThreads) {
+        const int part = j / a.k, r = j - part * a.k;
+        const int64_t src = ((int64_t)part * a.B + row) * a.k + r;
+        out[j] = make_key(a.V[src], a.I[src]);
+    }
+    if (threadIdx.x == 0) a.list_cnt[row * kCntStride] = n;
 }
 
 // ---------------------------------------------------------------------------
@@ -706,6 +724,12 @@ hipError_t launch_thr(const ThrArgs& a, int64_t rows, hipStream_t st)
 hipError_t launch_read_probe(const void* buf, int64_t n16, uint32_t* sink, int ncu, hipStream_t st)
 {
     launch(read_probe_kernel, dim3((unsigned)(2 * ncu)), dim3(kProbeThreads), 0, st, (const u32x4*)buf, n16, sink);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack(const PackArgs& a, int64_t rows, hipStream_t st)
+{
+    launch(pack_kernel, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     return hipGetLastError();
 }
 

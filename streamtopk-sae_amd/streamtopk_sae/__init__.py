@@ -6,7 +6,7 @@ Computes top_k(X @ W_enc.T + b_enc, k) per row without materialising the
 of the reference are not part of this build.
 """
 from streamtopk_sae.reference import reference_topk_sae
-from streamtopk_sae.ops import topk_sae_cpu, topk_sae_cuda_exact, topk_sae_cuda_approx
+from streamtopk_sae.ops import topk_sae_cpu, topk_sae_cuda_exact, topk_sae_cuda_approx, merge_topk_shards
 from streamtopk_sae.utils import recall_at_k, str_to_dtype
 from streamtopk_sae.inputs import make_inputs
 
@@ -15,6 +15,7 @@ __all__ = [
     "topk_sae_cpu",
     "topk_sae_cuda_exact",
     "topk_sae_cuda_approx",
+    "merge_topk_shards",
     "recall_at_k",
     "str_to_dtype",
     "make_inputs",

@@ -136,9 +136,11 @@ def _device_inputs(X, W_enc, b_enc):
     return _aligned(X), _aligned(W_enc), b_enc
 
 
-def exact_forward(X, W_enc, b_enc, k):
+def exact_forward(X, W_enc, b_enc, k, f_offset=0):
     """The native exact forward (streamtopk_exact.cu:788-833): contiguous device
-    tensors, fp32 b_enc; returns (V fp32 (B,k), I int32 (B,k))."""
+    tensors, fp32 b_enc; returns (V fp32 (B,k), I int32 (B,k)).  A non-zero
+    f_offset marks W_enc / b_enc as latents f_offset .. f_offset+F-1 of a
+    larger dictionary (one shard): the indices are global."""
     lib = _lib.load()
     X, W_enc, b_enc = _device_inputs(X, W_enc, b_enc)
     B, d = X.shape
@@ -151,21 +153,66 @@ def exact_forward(X, W_enc, b_enc, k):
         I = torch.empty((B, k), dtype=torch.int32, device=X.device)
         ws = torch.empty(max(nbytes.value, 1), dtype=torch.uint8, device=X.device)
         stream = torch.cuda.current_stream(X.device).cuda_stream
-        rc = lib.stk_exact_forward(_ptr(X), _ptr(W_enc), _ptr(b_enc), _ptr(V), _ptr(I),
-                                   B, d, F, k, dt, _ptr(ws), ws.numel(), ctypes.c_void_p(stream))
+        if f_offset:
+            rc = lib.stk_exact_forward_shard(_ptr(X), _ptr(W_enc), _ptr(b_enc), _ptr(V), _ptr(I),
+                                             B, d, F, k, dt, int(f_offset), _ptr(ws), ws.numel(),
+                                             ctypes.c_void_p(stream))
+        else:
+            rc = lib.stk_exact_forward(_ptr(X), _ptr(W_enc), _ptr(b_enc), _ptr(V), _ptr(I),
+                                       B, d, F, k, dt, _ptr(ws), ws.numel(), ctypes.c_void_p(stream))
         _lib.check(rc)
     return V, I
 
 
-def topk_sae_cuda_exact(X, W_enc, b_enc, k):
+def topk_sae_cuda_exact(X, W_enc, b_enc, k, *, f_offset=0):
     """Exact streaming top-k SAE forward on the GPU (fp16, bf16, fp32; b_enc fp32).
 
     Returns values (B, k) fp32 and indices (B, k) int32 on X's device.
+    ``f_offset`` (keyword only, no counterpart in the reference): W_enc and
+    b_enc are latents ``f_offset .. f_offset + F - 1`` of a larger dictionary,
+    e.g. one GPU's shard, and the returned indices are global; combine the
+    shards' results with :func:`merge_topk_shards`.
     """
     _lib.load()
     if b_enc.dtype != torch.float32:
         b_enc = b_enc.float()
-    return exact_forward(X.contiguous(), W_enc.contiguous(), b_enc.contiguous(), k)
+    if f_offset < 0:
+        raise RuntimeError("f_offset must be >= 0")
+    return exact_forward(X.contiguous(), W_enc.contiguous(), b_enc.contiguous(), k, f_offset=f_offset)
+
+
+def merge_topk_shards(values, indices, k):
+    """Top-k of per-shard top-k results (no counterpart in the reference).
+
+    ``values`` / ``indices``: sequences of (B, k) fp32 / int32 device tensors
+    (or stacked (nparts, B, k) tensors) with global latent indices, e.g. the
+    outputs of ``topk_sae_cuda_exact(..., f_offset=...)`` over the shards of
+    W_enc gathered on one device.  Returns (values (B, k) fp32, indices (B, k)
+    int32), rows sorted by value descending, equal values by lower index.
+    """
+    lib = _lib.load()
+    Vp = values if torch.is_tensor(values) else torch.stack(list(values))
+    Ip = indices if torch.is_tensor(indices) else torch.stack(list(indices))
+    if Vp.dim() != 3 or tuple(Ip.shape) != tuple(Vp.shape):
+        raise RuntimeError("expected matching (nparts, B, k) values and indices")
+    if Vp.dtype != torch.float32 or Ip.dtype != torch.int32:
+        raise RuntimeError("values must be fp32 and indices int32")
+    if not Vp.is_cuda or Ip.device != Vp.device:
+        raise RuntimeError("values and indices must be on the same CUDA device")
+    if Vp.shape[2] != k:
+        raise RuntimeError("each part must hold k entries per row")
+    Vp, Ip = Vp.contiguous(), Ip.contiguous()
+    nparts, B, _ = Vp.shape
+    with torch.cuda.device(Vp.device):
+        nbytes = ctypes.c_size_t(0)
+        _lib.check(lib.stk_topk_merge_workspace_bytes(B, k, nparts, ctypes.byref(nbytes)))
+        V = torch.empty((B, k), dtype=torch.float32, device=Vp.device)
+        I = torch.empty((B, k), dtype=torch.int32, device=Vp.device)
+        ws = torch.empty(max(nbytes.value, 1), dtype=torch.uint8, device=Vp.device)
+        stream = torch.cuda.current_stream(Vp.device).cuda_stream
+        _lib.check(lib.stk_topk_merge(_ptr(Vp), _ptr(Ip), nparts, B, k, _ptr(V), _ptr(I),
+                                      _ptr(ws), ws.numel(), ctypes.c_void_p(stream)))
+    return V, I
 
 
 def approx_forward(X, W_enc, b_enc, k, c, candidate_buffer=None, candidates=False):

@@ -81,3 +81,33 @@ def test_cpu_forward_through_abi():
     check_against_scores(V, I, oracle.scores_f64(X, W, b), 16, 1e-5, "abi cpu")
     assert lib.stk_cpu_forward(p(X), p(W), p(b), p(V), p(I), 5, 48, 300, 5, 2) == 1
     assert "unsupported k=5" in lib.stk_last_error().decode()
+
+
+def _shard(f_offset, F=256, k=8):
+    lib = _lib.load()
+    return lib.stk_exact_forward_shard(None, None, None, None, None, 4, 64, F, k, 2, f_offset, None, 0, None)
+
+
+@pytest.mark.parametrize("f_offset,F,msg", [
+    (-1, 256, "f_offset=-1 out of range"),
+    (0x7FFFFFFF - 100, 256, "exceeds the int32 index range"),
+])
+def test_shard_offset_errors(f_offset, F, msg):
+    assert _shard(f_offset, F) == 1
+    assert msg in _lib.load().stk_last_error().decode()
+
+
+def test_merge_workspace_and_errors():
+    lib = _lib.load()
+    nb = ctypes.c_size_t(0)
+    # dense candidate lists of nparts*k keys per row (256-byte aligned), then one
+    # 128-byte count line per row
+    assert lib.stk_topk_merge_workspace_bytes(4, 8, 3, ctypes.byref(nb)) == 0
+    assert nb.value == 4 * 24 * 8 + 4 * 32 * 4
+    assert lib.stk_topk_merge_workspace_bytes(0, 8, 3, ctypes.byref(nb)) == 0 and nb.value == 0
+    for B, k, nparts, msg in [(4, 3, 2, "unsupported k=3"), (4, 8, 0, "nparts=0 out of range"),
+                              (4, 128, 9000, "nparts=9000 out of range")]:
+        assert lib.stk_topk_merge_workspace_bytes(B, k, nparts, ctypes.byref(nb)) == 1
+        assert msg in lib.stk_last_error().decode()
+    rc = lib.stk_topk_merge(None, None, 2, 4, 8, None, None, None, 0, None)
+    assert rc == 1 and "null tensor pointer" in lib.stk_last_error().decode()
