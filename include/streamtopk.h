@@ -117,7 +117,8 @@ int stk_cpu_forward(const float* X, const float* W, const float* b, float* V, in
 /* Plain HBM read stream (no counterpart in the reference; used by bench.py to
  * report the streaming kernels' bandwidth as a fraction of a measured read
  * stream): reads `bytes` (a multiple of 16) from the 16-byte aligned device
- * buffer `buf` once, with coalesced nontemporal loads, and XORs a digest of
+ * buffer `buf` once (as 4 KiB rows, one 128-byte line of each of 256 rows
+ * per round, nontemporal loads: the fastest plain read order measured), and XORs a digest of
  * it into *sink (a device uint32), asynchronously on `stream`.  Timed under
  * the name "read_probe". */
 int stk_read_probe(const void* buf, size_t bytes, uint32_t* sink, void* stream);

@@ -615,29 +615,65 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(PackArgs a)
 
 // ---------------------------------------------------------------------------
 // read_probe_kernel: reads n16 16-byte words once and folds them (XOR) into
-// *sink with one atomic per wave, so that no load can be elided.  Each
-// workgroup streams one contiguous chunk, 64 KiB per round (eight coalesced
-// 8 KiB loads in flight per thread), with nontemporal loads (the fastest plain
-// stream measured on MI355X): the HBM read rate the streaming kernels are
-// compared with.
+// *sink with one atomic per wave, so that no load can be elided.  The words
+// are taken as 4 KiB rows; each workgroup owns a contiguous run of rows and
+// reads them 256 rows at a time, one 128-byte line of each row per round (four
+// nontemporal 16-byte loads per thread), two rounds in flight.  Of the plain
+// read orders measured on MI355X (this one, 32 KiB contiguous per round, and
+// 256-byte pieces of 128 rows), this one is the fastest, ~7.1 TB/s over 1 GiB:
+// it is the HBM read rate the streaming kernels are compared with.  Words past
+// the last whole row are read by workgroup 0.
 // ---------------------------------------------------------------------------
 constexpr int kProbeThreads = 512;
+constexpr int kProbeRow = 256;   // 16-byte words per 4 KiB row
 
 __global__ __launch_bounds__(kProbeThreads) void read_probe_kernel(const u32x4* p, int64_t n16, uint32_t* sink)
 {
-    const int64_t per = (n16 + gridDim.x - 1) / gridDim.x;
-    const int64_t lo = (int64_t)blockIdx.x * per;
-    const int64_t hi = lo + per < n16 ? lo + per : n16;
+    const int tid = threadIdx.x;
+    const int64_t nrows = n16 / kProbeRow;
+    const int64_t per = (nrows + gridDim.x - 1) / gridDim.x;
+    int64_t r0 = (int64_t)blockIdx.x * per, r1 = r0 + per;
+    r0 = r0 < nrows ? r0 : nrows;
+    r1 = r1 < nrows ? r1 : nrows;
     u32x4 acc = {0u, 0u, 0u, 0u};
-    int64_t i = lo + threadIdx.x;
-    for (; i + 7 * kProbeThreads < hi; i += 8 * kProbeThreads) {
-        u32x4 v[8];
+    for (int64_t t0 = r0; t0 < r1; t0 += 256) {
+        const int64_t nr = r1 - t0 < 256 ? r1 - t0 : 256;
+        // round s: words 8s .. 8s+7 of each of the tile's rows; thread chunk c is
+        // row c / 8, word c % 8 of the round.  Chunks of rows past the tile's end
+        // load row 0 again (so that every load is unconditional) and are masked
+        // out when folded.
+        bool ok[4];
+        int64_t off[4];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(p + i + u * kProbeThreads);
+        for (int q = 0; q < 4; ++q) {
+            const int c = tid + kProbeThreads * q;
+            ok[q] = (c >> 3) < nr;
+            off[q] = (t0 + (ok[q] ? (c >> 3) : 0)) * kProbeRow + (c & 7);
+        }
+        auto load = [&](u32x4 (&v)[4], int s) {
 #pragma unroll
-        for (int u = 0; u < 8; ++u) acc ^= v[u];
+            for (int q = 0; q < 4; ++q) v[q] = __builtin_nontemporal_load(p + off[q] + 8 * s);
+        };
+        auto fold = [&](const u32x4 (&v)[4]) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc ^= ok[q] ? v[q] : u32x4{0u, 0u, 0u, 0u};
+        };
+        u32x4 va[4], vb[4];
+        load(va, 0);
+        load(vb, 1);
+        for (int s = 2; s < kProbeRow / 8; s += 2) {
+            fold(va);
+            load(va, s);
+            __syncthreads();
+            fold(vb);
+            load(vb, s + 1);
+            __syncthreads();
+        }
+        fold(va);
+        fold(vb);
     }
-    for (; i < hi; i += kProbeThreads) acc ^= __builtin_nontemporal_load(p + i);
+    if (blockIdx.x == 0)
+        for (int64_t i = nrows * kProbeRow + tid; i < n16; i += kProbeThreads) acc ^= __builtin_nontemporal_load(p + i);
     uint32_t x = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) x ^= __shfl_xor(x, off, 64);
@@ -723,7 +759,7 @@ hipError_t launch_thr(const ThrArgs& a, int64_t rows, hipStream_t st)
 
 hipError_t launch_read_probe(const void* buf, int64_t n16, uint32_t* sink, int ncu, hipStream_t st)
 {
-    launch(read_probe_kernel, dim3((unsigned)(2 * ncu)), dim3(kProbeThreads), 0, st, (const u32x4*)buf, n16, sink);
+    launch(read_probe_kernel, dim3((unsigned)ncu), dim3(kProbeThreads), 0, st, (const u32x4*)buf, n16, sink);
     return hipGetLastError();
 }
 
