@@ -17,11 +17,14 @@
 //   - The pipeline restarts at every tile, so the epilogue holds no prefetch.
 //   - bias: the tile's 256 values are loaded at the tile start and staged in
 //     LDS for the epilogue.
-//   - epilogue, one row block at a time: the accumulators are read once,
-//     biased, compared with the row threshold and staged in LDS; survivors
-//     go to the row's queue segment in global memory (counters in LDS).  A
-//     full segment is rank-compacted to its top-k, which raises the row
-//     threshold.
+//   - epilogue, one row block at a time and no barrier between blocks: the
+//     accumulators are read once, biased, compared with the row threshold
+//     and staged in LDS; each lane reserves its survivors' slots in the row's
+//     queue segment in global memory (counters in LDS), and the wave's
+//     survivors are spread over its lanes for the stores.  Survivors that
+//     find a segment full wait for one barrier per tile; then the full
+//     segments are rank-compacted to their top-k, which raises the row
+//     thresholds, and the rest is re-filtered and appended.
 //   - grid: workgroups are placed so that the row blocks sharing a W range
 //     run on one XCD (workgroup i runs on XCD i % 8), and W is fetched into
 //     that XCD's L2 once for all of them.
