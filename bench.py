@@ -8,6 +8,7 @@ topk_sae_cuda_exact over the resident batch.  Prints ONE JSON line.
   python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
 
 Workloads: c2_bf16 (default), c2_fp16, c2_fp32, c1_bf16, c3_approx_c{16,32,64,128},
+c3_cand_c{16,32,64,128} (the approximate op with its candidate buffer),
 c4_bf16, c4_bf16_heavy.  Only --gpus 1 is supported (one GPU per box).
 """
 import argparse
@@ -40,6 +41,10 @@ for _c in (16, 32, 64, 128):
     # the approximate op requires k <= c (streamtopk_approx.cu:248): c=16 runs at k=16
     WORKLOADS[f"c3_approx_c{_c}"] = dict(B=128, d=2048, F=1048576, k=min(32, _c), c=_c, dtype="bf16",
                                          op="approx", label=f"BASELINE config 3, c={_c}, k={min(32, _c)}")
+    # the same with the per-group candidate buffer requested (group_kernel + cand_kernel)
+    WORKLOADS[f"c3_cand_c{_c}"] = dict(B=128, d=2048, F=1048576, k=min(32, _c), c=_c, dtype="bf16",
+                                       op="approx_cand",
+                                       label=f"BASELINE config 3, c={_c}, k={min(32, _c)}, candidate buffer")
 
 
 def _cpu_cores():
@@ -193,12 +198,19 @@ def main():
         def step():
             return topk_sae_cuda_exact(X, W, b, k)
         main_name = "main_kernel"
-    else:
+    elif wl["op"] == "approx":
         c = wl["c"]
 
         def step():
             return topk_sae_cuda_approx(X, W, b, k, c)
         main_name = "main_kernel"
+    else:
+        c = wl["c"]
+        cand = torch.empty((B, (F + 127) // 128, c), dtype=torch.float32, device=dev)
+
+        def step():
+            return topk_sae_cuda_approx(X, W, b, k, c, candidate_buffer=cand)
+        main_name = "group_kernel"
 
     for _ in range(args.warmup):
         step()
@@ -226,13 +238,14 @@ def main():
                 out[name] = {"avg_us": 1e3 * tot.value / n.value, "launches": n.value}
         return out
 
-    kern = read_profile(("main_kernel",))
+    kern = read_profile((main_name,))
     # untimed breakdown pass: events around every kernel of the pipeline
     _lib.check(lib.stk_profile_enable(1))
     for _ in range(min(args.steps, 50)):
         step()
     torch.cuda.synchronize()
-    breakdown = read_profile(("sample_kernel", "thr_kernel", "main_kernel", "merge_kernel"))
+    breakdown = read_profile(("sample_kernel", "thr_kernel", "main_kernel", "merge_kernel", "group_kernel",
+                              "cand_kernel"))
     # a plain read stream over W's bytes, timed the same way: the measured
     # read ceiling the streaming kernel is compared with
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -253,6 +266,8 @@ def main():
     rows_per_s = B * args.steps / wall
     w_bytes = F * d * es
     alg_main = w_bytes + B * d * es + 4 * F                 # W + X + b streamed by main_kernel
+    if main_name == "group_kernel":
+        alg_main += 8 * B * ((F + 127) // 128) * wl["c"]    # + the candidate values and indices written
     alg_total = alg_main + 8 * B * k                        # + V, I (bench/run_bandwidth.py:73-77)
     flops = 2.0 * B * d * F
     main_us = kern[main_name]["avg_us"]
@@ -268,7 +283,7 @@ def main():
                 "unit": "TFLOP/s", "frac": round(tflops_main / MFMA_PEAK_TFLOPS[dtn], 4)}
     # batches of 512 rows or more run the large-batch kernel (mainl_kernel);
     # both are timed under the profile name main_kernel
-    kname = "mainl_kernel" if B >= 512 else "main_kernel"
+    kname = main_name if main_name != "main_kernel" else "mainl_kernel" if B >= 512 else "main_kernel"
     roof["kernel"] = kname
     roof["traffic"] = traffic_from_profile(kname, args.workload)
     roof["alg_bytes_per_launch"] = alg_main

@@ -592,7 +592,7 @@ int stk_approx_forward(const void* X, const void* W, const float* b, float* V, i
     if (e != hipSuccess) return hip_fail(e, "group_kernel launch");
     CandArgs ca;
     ca.cand_vals = cand_vals; ca.cand_idxs = cand_idxs;
-    ca.per_row = p.num_groups * c; ca.k = (int)k; ca.V = V; ca.I = I;
+    ca.num_groups = p.num_groups; ca.c = (int)c; ca.k = (int)k; ca.V = V; ca.I = I;
     pg = prof_begin("cand_kernel", st);
     e = launch_cand(ca, B, st);
     prof_end(pg, st);

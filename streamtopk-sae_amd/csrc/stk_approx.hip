@@ -2,159 +2,291 @@
 // variant that materialise the per-group candidates, for callers that ask for
 // the candidate buffer (streamtopk_approx.cu:264-274 side effect).
 //
-//   group_kernel : MFMA scores for 256 latents (two groups) x up to 128 rows per
-//                  tile, then per (row, group) a bitonic sort of the group's 128
-//                  keys in LDS; writes each group's top-c, descending, padded
+//   group_kernel : TileStream (W streamed once, MFMA scores for 256 latents =
+//                  two groups x up to 128 rows per tile); per 32-row block the
+//                  scores go to LDS as order-preserving words, then each
+//                  16-lane row of a wave sorts one (row, group)'s 128 keys in
+//                  registers (bitonic network: 8 keys per lane, lane exchanges
+//                  by DPP; 32-bit keys, with a 64-bit pass where truncated
+//                  scores tie) and writes the group's top-c, descending, padded
 //                  with (-FLT_MAX, -1) past the end of F
 //                  (streamtopk_approx.cu:42-167).
 //   cand_kernel  : per row, top-k over all group candidates -- the final
 //                  torch.topk + gather of the reference (ops.py:80-81), on the
-//                  device.
+//                  device.  Only the groups whose head reaches a lower bound of
+//                  the row's k-th largest candidate are read past their head.
 #include "stk_kernels.h"
+#include "stk_select.h"
 
 namespace stk {
 
+constexpr int kOrdStride = kGroupTile + 4;   // LDS words per staged row (pad: no bank conflicts)
+
 size_t group_lds_bytes(int NB)
 {
-    const size_t BT = 32 * (size_t)NB;
-    return 2 * BT * kXRowStride + 2 * 32 * kApproxGroup * sizeof(uint64_t);
+    const size_t rings = 2 * (size_t)kGroupTile * kXRowStride + 2 * 32 * (size_t)NB * kXRowStride;
+    return rings + 2 * kGroupTile * sizeof(float) + 32 * (size_t)kOrdStride * sizeof(uint32_t);
 }
 
-template <int DT, int NB>
-__global__ __launch_bounds__(kThreads, 1) void group_kernel(GroupArgs a)
+// Key of the lane X lanes away within its 16-lane row (X = 1, 2, 4, 8): lane
+// l gets lane l ^ X.  1 and 2 are quad permutations, 8 is a rotation of the
+// row by 8; 4 goes through the LDS crossbar.
+template <int X>
+__device__ __forceinline__ uint32_t row_xor(uint32_t v)
 {
-    constexpr int BT = 32 * NB;
-    constexpr int FRAGS = 2;
-    constexpr int ES = Dt<DT>::esize;
-    constexpr int DS = Dt<DT>::DS;
-    constexpr int G = kApproxGroup;
-    extern __shared__ __align__(16) unsigned char smem[];
-    unsigned char* xs0 = smem;
-    unsigned char* xs1 = smem + BT * kXRowStride;
-    uint64_t* keys = (uint64_t*)(smem + 2 * BT * kXRowStride);   // [2 groups][32 cols][G]
+    if constexpr (X == 4) {
+        return __shfl_xor(v, 4, 64);
+    } else {
+        constexpr int ctl = X == 1 ? 0xB1 : X == 2 ? 0x4E : 0x128;   // quad_perm [1,0,3,2], [2,3,0,1]; row_ror:8
+        return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, ctl, 0xF, 0xF, true);
+    }
+}
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int h = lane >> 5, jl = lane & 31;
-    const int64_t b0 = (int64_t)blockIdx.y * BT;
-    const int64_t B = a.B, d = a.d, F = a.F;
-    const int c = a.c;
+template <int X>
+__device__ __forceinline__ uint64_t row_xor(uint64_t v)
+{
+    const uint32_t lo = row_xor<X>((uint32_t)v), hi = row_xor<X>((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
 
-    MainLoop<DT, NB, FRAGS> ml;
-    ml.X = (const unsigned char*)a.X;
-    ml.B = B;
-    ml.d = d;
-    ml.b0 = b0;
-    ml.lane = lane;
-    ml.h = h;
-    const int64_t nds = (d + DS - 1) / DS;
-    const unsigned char* W = (const unsigned char*)a.W;
-    const int64_t num_tiles = (a.num_groups + 1) / 2;
-    const int64_t t0 = (int64_t)blockIdx.x * a.tiles_per_wg;
-    const int64_t t1 = (t0 + a.tiles_per_wg < num_tiles) ? t0 + a.tiles_per_wg : num_tiles;
-
-    for (int64_t tile = t0; tile < t1; ++tile) {
-        const int64_t fw0 = tile * kGroupTile + wave * 64;
+// One compare-exchange stage of the bitonic network over the 128 keys of a
+// 16-lane row; lane l holds entries 8l .. 8l+7 in v[0..7].  Blocks of SIZE
+// entries alternate direction, the block holding entry 0 descending, as in
+// the textbook network; partners are STRIDE entries apart.
+template <int SIZE, int STRIDE, class T>
+__device__ __forceinline__ void bitonic_stage(T (&v)[8], int l)
+{
+    if constexpr (STRIDE >= 8) {
+        constexpr int X = STRIDE / 8;
+        const bool lower = (l & X) == 0;
+        const bool desc = SIZE >= 128 ? true : (l & (SIZE / 8)) == 0;
+        const bool keep_max = lower == desc;
+        T o[8];
 #pragma unroll
-        for (int fa = 0; fa < FRAGS; ++fa) {
-            int64_t f = fw0 + fa * 32 + jl;
-            f = (f < F) ? f : F - 1;
-            ml.wrow[fa] = W + f * d * ES + h * 64;
+        for (int j = 0; j < 8; ++j) o[j] = row_xor<X>(v[j]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            // keys are distinct apart from the padding key 0
+            const T mx = o[j] > v[j] ? o[j] : v[j], mn = o[j] > v[j] ? v[j] : o[j];
+            v[j] = keep_max ? mx : mn;
         }
-        f32x16 acc[FRAGS][NB];
+    } else {
 #pragma unroll
-        for (int fa = 0; fa < FRAGS; ++fa)
-#pragma unroll
-            for (int n = 0; n < NB; ++n)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[fa][n][r] = 0.f;
-        ml.run(acc, 0, nds, xs0, xs1, tid);
-
-        float bias_r[FRAGS][16];
-#pragma unroll
-        for (int fa = 0; fa < FRAGS; ++fa)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t f = fw0 + fa * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-                bias_r[fa][r] = a.bias[f < F ? f : 0];
-            }
-
-#pragma unroll
-        for (int n = 0; n < NB; ++n) {
-            // keys of this 32-column block: group g = wave / 2, slot within group
-#pragma unroll
-            for (int fa = 0; fa < FRAGS; ++fa)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int lt = wave * 64 + fa * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-                    const int64_t f = tile * kGroupTile + lt;
-                    const int g = lt / G, p = lt % G;
-                    keys[((size_t)g * 32 + jl) * G + p] =
-                        (f < F) ? make_key(acc[fa][n][r] + bias_r[fa][r], f) : 0ull;
-                }
-            __syncthreads();
-            // bitonic sort (descending) of the 64 segments of G keys
-            for (int size = 2; size <= G; size <<= 1) {
-                for (int stride = size >> 1; stride > 0; stride >>= 1) {
-                    for (int t = tid; t < 64 * (G / 2); t += kThreads) {
-                        const int seg = t / (G / 2), u = t % (G / 2);
-                        const int i = 2 * u - (u & (stride - 1));
-                        const int jx = i + stride;
-                        uint64_t* sk = keys + (size_t)seg * G;
-                        const uint64_t x = sk[i], y = sk[jx];
-                        const bool desc = ((i & size) == 0);
-                        if (desc ? (x < y) : (x > y)) { sk[i] = y; sk[jx] = x; }
-                    }
-                    __syncthreads();
-                }
-            }
-            // emit the top-c of each group of this column block
-            for (int t = tid; t < 64 * c; t += kThreads) {
-                const int seg = t / c, e = t % c;
-                const int g = seg / 32, col = seg % 32;
-                const int64_t row = b0 + 32 * n + col;
-                const int64_t grp = tile * 2 + g;
-                if (row < B && grp < a.num_groups) {
-                    const uint64_t key = keys[(size_t)seg * G + e];
-                    const size_t o = ((size_t)row * a.num_groups + grp) * c + e;
-                    a.cand_vals[o] = key ? key_value(key) : -3.402823466e+38f;
-                    a.cand_idxs[o] = key ? key_index(key) : -1;
-                }
-            }
-            __syncthreads();
+        for (int j = 0; j < 8; ++j) {
+            if (j & STRIDE) continue;
+            const bool desc = SIZE >= 128 ? true : SIZE >= 8 ? (l & (SIZE / 8)) == 0 : (j & SIZE) == 0;
+            const T x = v[j], y = v[j + STRIDE];
+            const T mx = x > y ? x : y, mn = x > y ? y : x;
+            v[j] = desc ? mx : mn;
+            v[j + STRIDE] = desc ? mn : mx;
         }
     }
 }
 
-// Per row: top-k over the (value, index) candidates of every group.
+template <int SIZE, int STRIDE, class T>
+__device__ __forceinline__ void bitonic_merge(T (&v)[8], int l)
+{
+    bitonic_stage<SIZE, STRIDE>(v, l);
+    if constexpr (STRIDE > 1) bitonic_merge<SIZE, STRIDE / 2>(v, l);
+}
+
+// Sorts the row's 128 keys into descending order: entry e = 8l + j.
+template <int SIZE = 128, class T>
+__device__ __forceinline__ void bitonic_sort128(T (&v)[8], int l)
+{
+    if constexpr (SIZE > 2) bitonic_sort128<SIZE / 2, T>(v, l);
+    bitonic_merge<SIZE, SIZE / 2>(v, l);
+}
+
+template <int DT, int NB>
+__global__ __launch_bounds__(kMainThreads, 1) void group_kernel(GroupArgs a)
+{
+    using TS = TileStream<DT, NB, kMainWaves>;
+    static_assert(TS::kTileF == kGroupTile && kGroupTile == 2 * kApproxGroup, "one tile is two groups");
+    extern __shared__ __align__(16) unsigned char smem[];
+    float* bias_lds = (float*)(smem + TS::kRingBytes);             // [2][kGroupTile]
+    uint32_t* ordv = (uint32_t*)(bias_lds + 2 * kGroupTile);       // [32 rows][kOrdStride]
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = lane >> 5, jl = lane & 31;
+    const int l = lane & 15, sq = lane >> 4;
+    const int64_t b0 = (int64_t)blockIdx.y * (32 * NB);
+    const int64_t B = a.B, F = a.F, G = a.num_groups;
+    const int c = a.c;
+    const int64_t num_tiles = (G + 1) / 2;
+
+    TS ts;
+    ts.W = (const unsigned char*)a.W;
+    ts.w_row_bytes = a.d * Dt<DT>::esize;
+    ts.bias = a.bias;
+    ts.F = F;
+    ts.tile_begin = (int64_t)blockIdx.x * a.tiles_per_wg;
+    {
+        const int64_t t1 = ts.tile_begin + a.tiles_per_wg;
+        ts.ntiles = (int)((t1 < num_tiles ? t1 : num_tiles) - ts.tile_begin);
+    }
+    ts.nds = (int)(a.d / Dt<DT>::DS);
+    ts.nds2 = (ts.nds + 1) / 2 * 2;
+    ts.tid = tid;
+    ts.lane = lane;
+    ts.wave = wave;
+    ts.h = h;
+    ts.jl = jl;
+    ts.init_x((const unsigned char*)a.X, B, b0, a.d);
+
+    f32x16 acc[NB];
+    ts.run(acc, smem, bias_lds, [&](int t, f32x16 (&ac)[NB], const float (&bias_r)[16]) {
+        const int64_t tile = ts.tile_begin + t;
+        const int64_t f0 = tile * kGroupTile;
+        // accumulator register r of this lane: row 32n + jl, latent lt0 + 8*(r/4) + r%4
+        const int lt0 = wave * 32 + h * 4;
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            if (n > 0) __syncthreads();   // the previous block's keys are read
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                u32x4 o;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 4 * q + i;
+                    o[i] = (f0 + lt0 + 8 * q + i < F) ? ordered_u32(ac[n][r] + bias_r[r]) : 0u;
+                }
+                *(u32x4*)(ordv + jl * kOrdStride + lt0 + 8 * q) = o;
+            }
+            __syncthreads();
+            // 64 (row, group) segments per block, 4 per wave and round
+#pragma unroll
+            for (int rd = 0; rd < 2; ++rd) {
+                const int seg = wave * 8 + rd * 4 + sq;
+                const int rl = seg >> 1, g = seg & 1;
+                const uint32_t* src = ordv + rl * kOrdStride + g * kApproxGroup;
+                const u32x4 w0 = *(const u32x4*)(src + 8 * l), w1 = *(const u32x4*)(src + 8 * l + 4);
+                // Short keys: the ordered word with its low 7 bits replaced by
+                // 127 - position, so equal truncated words go to the lower
+                // position; padding (word 0) sorts last.  Entries with equal
+                // truncated words end up adjacent, so unless two such real
+                // entries meet within the first c + 1, the short order is the
+                // exact one.
+                uint32_t v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    v[j] = ((j < 4 ? w0[j] : w1[j - 4]) & ~0x7Fu) | (uint32_t)(127 - (8 * l + j));
+                bitonic_sort128(v, l);
+                const uint32_t nx = __shfl_down(v[0], 1, 16);   // entry 8l + 8
+                bool tie = false;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t y = j < 7 ? v[j + 1] : nx;
+                    const bool last = j == 7 && l == 15;
+                    tie |= !last && 8 * l + j < c && (y >> 7) != 0 && (v[j] >> 7) == (y >> 7);
+                }
+                float val[8];
+                uint32_t idx[8];
+                const uint32_t fg = (uint32_t)(f0 + g * kApproxGroup);
+                if (__ballot(tie) == 0) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const uint32_t pos = 127u - (v[j] & 0x7Fu);
+                        const bool real = (v[j] >> 7) != 0;
+                        val[j] = real ? key_value((uint64_t)src[pos] << 32) : -3.402823466e+38f;
+                        idx[j] = real ? fg + pos : 0xFFFFFFFFu;
+                    }
+                } else {
+                    // full keys for this wave's four segments
+                    uint64_t u[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const uint32_t ov = j < 4 ? w0[j] : w1[j - 4];
+                        u[j] = ov ? (((uint64_t)ov << 32) | (0xFFFFFFFFu - (fg + 8 * l + j))) : 0ull;
+                    }
+                    bitonic_sort128(u, l);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        val[j] = u[j] ? key_value(u[j]) : -3.402823466e+38f;
+                        idx[j] = u[j] ? (uint32_t)key_index(u[j]) : 0xFFFFFFFFu;
+                    }
+                }
+                const int64_t row = b0 + 32 * n + rl;
+                const int64_t grp = 2 * tile + g;
+                if (row < B && grp < G && 8 * l < c) {
+                    const int64_t o = (row * G + grp) * c + 8 * l;
+                    *(f32x4*)(a.cand_vals + o) = f32x4{val[0], val[1], val[2], val[3]};
+                    *(f32x4*)(a.cand_vals + o + 4) = f32x4{val[4], val[5], val[6], val[7]};
+                    *(u32x4*)(a.cand_idxs + o) = u32x4{idx[0], idx[1], idx[2], idx[3]};
+                    *(u32x4*)(a.cand_idxs + o + 4) = u32x4{idx[4], idx[5], idx[6], idx[7]};
+                }
+            }
+        }
+    });
+}
+
+// Key of group g's head (its largest candidate), 0 for a padded group.
+__device__ __forceinline__ uint64_t head_key(const float* cv, const int32_t* ci, int64_t g, int64_t G, int c)
+{
+    const int64_t gg = g < G ? g : G - 1;
+    const int32_t idx = ci[gg * c];
+    const float val = cv[gg * c];
+    return (g < G && idx >= 0) ? make_key(val, idx) : 0ull;
+}
+
+// Per row: top-k over the (value, index) candidates of every group.  Each
+// group's candidates are in descending order, so the row's top k lie among
+// the first k of every group, and a group whose head is below a key that k
+// candidates reach holds none of them.  The heads' k-th largest maximum over
+// the threads is such a key.
 __global__ __launch_bounds__(kThreads) void cand_kernel(CandArgs a)
 {
     __shared__ SelShared S;
+    constexpr int U = 8;   // groups per thread whose heads are loaded together
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
-    const int k = a.k;
-    if (tid == 0) { S.cnt = 0; S.thr = 0; }
+    const int k = a.k, c = a.c;
+    const int64_t G = a.num_groups;
+    const float* cv = a.cand_vals + row * G * c;
+    const int32_t* ci = a.cand_idxs + row * G * c;
+
+    uint64_t m = 0;
+    for (int64_t g0 = tid; g0 < G; g0 += U * kThreads) {
+        uint64_t hk[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) hk[u] = head_key(cv, ci, g0 + u * kThreads, G, c);
+#pragma unroll
+        for (int u = 0; u < U; ++u) m = hk[u] > m ? hk[u] : m;
+    }
+    const uint64_t T = kth_of_maxima(S, m, k, tid);   // >= 1; k candidates are >= T
+    if (tid == 0) { S.cnt = 0; S.thr = T - 1; }
     __syncthreads();
-    int64_t cur = tid;
-    const float* cv = a.cand_vals + row * a.per_row;
-    const int32_t* ci = a.cand_idxs + row * a.per_row;
+
+    const int kk = k < c ? k : c;
+    int64_t g0 = tid;
+    int u0 = 0, e0 = 0;   // resume point after a full buffer
     for (;;) {
         const uint64_t thr = S.thr;
         bool stalled = false;
-        while (cur < a.per_row) {
-            const int32_t idx = ci[cur];
-            if (idx >= 0) {
-                const uint64_t key = make_key(cv[cur], idx);
-                if (key > thr) {
+        for (; g0 < G; g0 += U * kThreads, u0 = 0, e0 = 0) {
+            uint64_t hk[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) hk[u] = head_key(cv, ci, g0 + u * kThreads, G, c);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (stalled || u < u0 || hk[u] <= thr) continue;
+                const int64_t base = (g0 + u * kThreads) * c;
+                for (int e = (u == u0 ? e0 : 0); e < kk; ++e) {
+                    const int32_t idx = ci[base + e];
+                    if (idx < 0) break;
+                    const uint64_t key = make_key(cv[base + e], idx);
+                    if (key <= thr) break;
                     const int pos = atomicAdd(&S.cnt, 1);
-                    if (pos < kSelCap) {
-                        S.buf[pos] = key;
-                    } else {
+                    if (pos >= kSelCap) {
                         stalled = true;
+                        u0 = u;
+                        e0 = e;
                         break;
                     }
+                    S.buf[pos] = key;
                 }
             }
-            cur += kThreads;
+            if (stalled) break;
         }
         __syncthreads();
         if (S.cnt >= kSelCap) select_compact(S, kSelCap, k, tid);
@@ -163,10 +295,10 @@ __global__ __launch_bounds__(kThreads) void cand_kernel(CandArgs a)
     const int n = S.cnt < kSelCap ? S.cnt : kSelCap;
     if (n > k) select_compact(S, n, k, tid);
     __syncthreads();
-    const int m = n < k ? n : k;
-    if (tid < m) {
+    const int mk = n < k ? n : k;
+    if (tid < mk) {
         const uint64_t key = S.buf[tid];
-        const int r = rank_desc(S, m, key);
+        const int r = rank_desc(S, mk, key);
         a.V[row * k + r] = key_value(key);
         a.I[row * k + r] = key_index(key);
     }
@@ -179,7 +311,7 @@ static hipError_t launch_group_t(const GroupArgs& a, dim3 grid, hipStream_t st)
     auto kern = group_kernel<DT, NB>;
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    launch(kern, grid, dim3(kThreads), lds, st, a);
+    launch(kern, grid, dim3(kMainThreads), lds, st, a);
     return hipGetLastError();
 }
 

@@ -174,8 +174,8 @@ struct GroupArgs {               // approximate variant, per-group top-c candida
 struct CandArgs {                // approximate variant, top-k over the candidates
     const float* cand_vals;
     const int32_t* cand_idxs;
-    int64_t per_row;             // num_groups * c
-    int k;
+    int64_t num_groups;          // candidates per row: num_groups * c, each group's in descending order
+    int c, k;
     float* V;
     int32_t* I;
 };

@@ -95,3 +95,43 @@ def test_approx_known_answers(cuda_dev, with_buffer):
             cb = torch.empty((X.shape[0], (W.shape[0] + 127) // 128, c), dtype=torch.float32, device=cuda_dev)
         V, I = topk_sae_cuda_approx(Xt, Wt, bt, k, c, candidate_buffer=cb)
         assert np.array_equal(V.cpu().numpy(), Vk) and np.array_equal(I.cpu().numpy(), Ik)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("B,F,c", [(100, 5000, 32), (40, 3000, 128), (5, 2000, 16), (130, 1280, 64)])
+def test_approx_candidates_shapes(cuda_dev, dtype, B, F, c):
+    """Ragged batches (one, two and four 32-row blocks; a partial second row
+    block), F not a multiple of the 256-latent tile, every dtype: per-group
+    candidates against the oracle's, in descending order, and the final top-k
+    equal to the exact kernel's."""
+    print(f"case approx candidates {dtype} B={B} F={F} c={c}", flush=True)
+    d, k = 128, min(16, c)
+    tol = 1e-5 if dtype == torch.float32 else 2e-3
+    X, W, b = make_inputs(B, d, F, dtype, seed=25, device=cuda_dev)
+    nt = (F + 127) // 128
+    cb = torch.empty((B, nt, c), dtype=torch.float32, device=cuda_dev)
+    V, I = topk_sae_cuda_approx(X, W, b, k, c, candidate_buffer=cb)
+    _, _, cvo, cio = oracle.approx(_np(X), _np(W), _np(b), k, c, with_candidates=True)
+    cbn = cb.cpu().numpy()
+    pad = cio < 0
+    assert np.array_equal(cbn[pad], cvo[pad])
+    err = np.abs(cbn[~pad] - cvo[~pad]) / np.maximum(np.abs(cvo[~pad]), 1.0)
+    assert err.max() <= tol
+    assert np.all(np.diff(cbn, axis=2) <= 0)
+    Ve, Ie = topk_sae_cuda_exact(X, W, b, k)
+    assert torch.equal(V, Ve) and torch.equal(I, Ie)
+
+
+def test_approx_candidates_equal_scores(cuda_dev):
+    """All scores equal (X = 0, constant b_enc): ties go to the lower index, and
+    the groups that reach the row bound hold more candidates than one
+    selection buffer, so the final selection compacts and resumes."""
+    print("case approx candidates equal scores", flush=True)
+    B, d, F, k, c = 4, 64, 51200, 32, 32
+    X = torch.zeros((B, d), dtype=torch.bfloat16, device=cuda_dev)
+    _, W, _ = make_inputs(B, d, F, torch.bfloat16, seed=26, device=cuda_dev)
+    b = torch.full((F,), 0.5, dtype=torch.float32, device=cuda_dev)
+    cb = torch.empty((B, F // 128, c), dtype=torch.float32, device=cuda_dev)
+    V, I = topk_sae_cuda_approx(X, W, b, k, c, candidate_buffer=cb)
+    assert torch.equal(I.cpu(), torch.arange(k, dtype=torch.int32).expand(B, k))
+    assert bool((V == 0.5).all()) and bool((cb == 0.5).all())
