@@ -122,6 +122,29 @@ def test_approx_candidates_shapes(cuda_dev, dtype, B, F, c):
     assert torch.equal(V, Ve) and torch.equal(I, Ie)
 
 
+@pytest.mark.parametrize("dtype,d,F,c", [(torch.bfloat16, 64, 100, 128), (torch.float32, 32, 700, 16)])
+def test_approx_candidates_small(cuda_dev, dtype, d, F, c):
+    """F below one group (one tile, mostly padding) and the narrowest fp32 row
+    (one d-step)."""
+    print(f"case approx candidates small {dtype} d={d} F={F} c={c}", flush=True)
+    B, k = 3, 16
+    tol = 1e-5 if dtype == torch.float32 else 2e-3
+    X, W, b = make_inputs(B, d, F, dtype, seed=27, device=cuda_dev)
+    nt = (F + 127) // 128
+    cb = torch.empty((B, nt, c), dtype=torch.float32, device=cuda_dev)
+    V, I = topk_sae_cuda_approx(X, W, b, k, c, candidate_buffer=cb)
+    _, _, cvo, cio = oracle.approx(_np(X), _np(W), _np(b), k, c, with_candidates=True)
+    cbn = cb.cpu().numpy()
+    pad = cio < 0
+    # padded slots per row: c minus the real latents of each group, where negative none
+    assert pad.sum() == B * sum(max(0, c - min(128, F - 128 * g)) for g in range(nt))
+    assert np.array_equal(cbn[pad], cvo[pad])
+    err = np.abs(cbn[~pad] - cvo[~pad]) / np.maximum(np.abs(cvo[~pad]), 1.0)
+    assert err.max() <= tol
+    Ve, Ie = topk_sae_cuda_exact(X, W, b, k)
+    assert torch.equal(V, Ve) and torch.equal(I, Ie)
+
+
 def test_approx_candidates_equal_scores(cuda_dev):
     """All scores equal (X = 0, constant b_enc): ties go to the lower index, and
     the groups that reach the row bound hold more candidates than one
