@@ -6,8 +6,8 @@
 //                  two groups x up to 128 rows per tile); per 32-row block the
 //                  scores go to LDS as order-preserving words, then each
 //                  16-lane row of a wave sorts one (row, group)'s 128 keys in
-//                  registers (bitonic network: 8 keys per lane, lane exchanges
-//                  by DPP; 32-bit keys, with a 64-bit pass where truncated
+//                  registers (bitonic network, one-direction form: 8 keys per
+//                  lane, lane exchanges by DPP; 32-bit keys, with a 64-bit pass where truncated
 //                  scores tie) and writes the group's top-c, descending, padded
 //                  with (-FLT_MAX, -1) past the end of F
 //                  (streamtopk_approx.cu:42-167).
@@ -28,16 +28,18 @@ size_t group_lds_bytes(int NB)
     return rings + 2 * kGroupTile * sizeof(float) + 32 * (size_t)kOrdStride * sizeof(uint32_t);
 }
 
-// Key of the lane X lanes away within its 16-lane row (X = 1, 2, 4, 8): lane
-// l gets lane l ^ X.  1 and 2 are quad permutations, 8 is a rotation of the
-// row by 8; 4 goes through the LDS crossbar.
+// Key of lane l ^ X within the lane's 16-lane row, X = 1 .. 15.  XOR 1, 3
+// and 2 are quad permutations, 7 and 15 mirror the half row and the row, 8
+// rotates the row by 8; 4 goes through the LDS crossbar.
 template <int X>
 __device__ __forceinline__ uint32_t row_xor(uint32_t v)
 {
+    static_assert(X == 1 || X == 2 || X == 3 || X == 4 || X == 7 || X == 8 || X == 15, "lane exchange");
     if constexpr (X == 4) {
         return __shfl_xor(v, 4, 64);
     } else {
-        constexpr int ctl = X == 1 ? 0xB1 : X == 2 ? 0x4E : 0x128;   // quad_perm [1,0,3,2], [2,3,0,1]; row_ror:8
+        // quad_perm [1,0,3,2], [2,3,0,1], [3,2,1,0]; row_half_mirror; row_ror:8; row_mirror
+        constexpr int ctl = X == 1 ? 0xB1 : X == 2 ? 0x4E : X == 3 ? 0x1B : X == 7 ? 0x141 : X == 8 ? 0x128 : 0x140;
         return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, ctl, 0xF, 0xF, true);
     }
 }
@@ -49,45 +51,60 @@ __device__ __forceinline__ uint64_t row_xor(uint64_t v)
     return ((uint64_t)hi << 32) | lo;
 }
 
-// One compare-exchange stage of the bitonic network over the 128 keys of a
-// 16-lane row; lane l holds entries 8l .. 8l+7 in v[0..7].  Blocks of SIZE
-// entries alternate direction, the block holding entry 0 descending, as in
-// the textbook network; partners are STRIDE entries apart.
-template <int SIZE, int STRIDE, class T>
-__device__ __forceinline__ void bitonic_stage(T (&v)[8], int l)
+// The bitonic network in its one-direction form, over the 128 keys of a
+// 16-lane row; lane l holds entries 8l .. 8l+7 in v[0..7].  Merging sorted
+// blocks of SIZE/2 into blocks of SIZE starts with a flip (entry e against
+// the mirrored entry e ^ (SIZE-1)) and continues with half-cleaners (e against
+// e ^ STRIDE); every comparator puts the larger key at the lower entry, so
+// the result is descending.  Keys are distinct apart from the padding key 0.
+template <class T>
+__device__ __forceinline__ T kmax(T a, T b) { return a > b ? a : b; }
+template <class T>
+__device__ __forceinline__ T kmin(T a, T b) { return a > b ? b : a; }
+
+template <int SIZE, class T>
+__device__ __forceinline__ void bitonic_flip(T (&v)[8], int l)
 {
-    if constexpr (STRIDE >= 8) {
-        constexpr int X = STRIDE / 8;
-        const bool lower = (l & X) == 0;
-        const bool desc = SIZE >= 128 ? true : (l & (SIZE / 8)) == 0;
-        const bool keep_max = lower == desc;
-        T o[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = row_xor<X>(v[j]);
+    if constexpr (SIZE <= 8) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            // keys are distinct apart from the padding key 0
-            const T mx = o[j] > v[j] ? o[j] : v[j], mn = o[j] > v[j] ? v[j] : o[j];
-            v[j] = keep_max ? mx : mn;
+            const int p = j ^ (SIZE - 1);
+            if (p < j) continue;
+            const T x = v[j], y = v[p];
+            v[j] = kmax(x, y);
+            v[p] = kmin(x, y);
         }
+    } else {
+        // partner: lane l ^ (SIZE/8 - 1), register 7 - j
+        const bool lower = (l & (SIZE / 16)) == 0;
+        T o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = row_xor<SIZE / 8 - 1>(v[7 - j]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = lower ? kmax(v[j], o[j]) : kmin(v[j], o[j]);
+    }
+}
+
+template <int STRIDE, class T>
+__device__ __forceinline__ void bitonic_half(T (&v)[8], int l)
+{
+    if constexpr (STRIDE >= 8) {
+        const bool lower = (l & (STRIDE / 8)) == 0;
+        T o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = row_xor<STRIDE / 8>(v[j]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = lower ? kmax(v[j], o[j]) : kmin(v[j], o[j]);
     } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             if (j & STRIDE) continue;
-            const bool desc = SIZE >= 128 ? true : SIZE >= 8 ? (l & (SIZE / 8)) == 0 : (j & SIZE) == 0;
             const T x = v[j], y = v[j + STRIDE];
-            const T mx = x > y ? x : y, mn = x > y ? y : x;
-            v[j] = desc ? mx : mn;
-            v[j + STRIDE] = desc ? mn : mx;
+            v[j] = kmax(x, y);
+            v[j + STRIDE] = kmin(x, y);
         }
     }
-}
-
-template <int SIZE, int STRIDE, class T>
-__device__ __forceinline__ void bitonic_merge(T (&v)[8], int l)
-{
-    bitonic_stage<SIZE, STRIDE>(v, l);
-    if constexpr (STRIDE > 1) bitonic_merge<SIZE, STRIDE / 2>(v, l);
+    if constexpr (STRIDE > 1) bitonic_half<STRIDE / 2>(v, l);
 }
 
 // Sorts the row's 128 keys into descending order: entry e = 8l + j.
@@ -95,7 +112,8 @@ template <int SIZE = 128, class T>
 __device__ __forceinline__ void bitonic_sort128(T (&v)[8], int l)
 {
     if constexpr (SIZE > 2) bitonic_sort128<SIZE / 2, T>(v, l);
-    bitonic_merge<SIZE, SIZE / 2>(v, l);
+    bitonic_flip<SIZE>(v, l);
+    if constexpr (SIZE >= 4) bitonic_half<SIZE / 4>(v, l);
 }
 
 template <int DT, int NB>

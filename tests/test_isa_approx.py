@@ -56,9 +56,12 @@ def test_sort_exchanges(asm, nb):
     body, meta = _kernel(asm, f"_ZN3stk12group_kernelILi2ELi{nb}EEEvNS_9GroupArgsE")
     assert int(re.search(r"\.vgpr_count:\s+(\d+)", meta).group(1)) <= 256
     dpp = len(re.findall(r"\bv_\w+_dpp\b", body))
-    # per sort: 8 of the 10 exchange stages are DPP (strides 8, 16, 64); per
-    # 32-row block two rounds of the 32-bit network and two of the 64-bit one
-    assert dpp >= nb * 2 * 8 * 8 * 3
-    assert "row_ror:8" in body and "quad_perm:[1,0,3,2]" in body and "quad_perm:[2,3,0,1]" in body
-    # stride 32 (two stages) of both networks, and the check's read of the next lane
-    assert body.count("ds_bpermute_b32") == nb * 2 * (2 * 8 + 1 + 2 * 8 * 2)
+    # per sort: 9 of the 10 exchange stages are DPP (the flips of 16 .. 128
+    # entries, the half-cleaners of strides 8 and 16); per 32-row block two
+    # rounds of the 32-bit network (8 keys per lane) and two of the 64-bit one
+    assert dpp >= nb * 2 * 9 * (8 + 16)
+    for ctl in ("row_mirror", "row_half_mirror", "quad_perm:[3,2,1,0]", "quad_perm:[1,0,3,2]",
+                "quad_perm:[2,3,0,1]"):
+        assert ctl in body, ctl
+    # stride 32 (one half-cleaner) of both networks, and the check's read of the next lane
+    assert body.count("ds_bpermute_b32") == nb * 2 * (8 + 1 + 16)
