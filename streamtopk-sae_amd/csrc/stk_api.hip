@@ -5,6 +5,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -100,6 +101,33 @@ static void prof_release()
 {
     for (auto& r : g_recs) { g_pool.push_back(r.a); g_pool.push_back(r.b); }
     g_recs.clear();
+}
+
+// Dynamic-LDS limits already raised, per (kernel, device).
+struct LdsLimit {
+    const void* kern;
+    int dev;
+    size_t lds;
+};
+static std::mutex g_lds_mu;
+static std::vector<LdsLimit> g_lds;
+
+hipError_t ensure_lds(const void* kern, size_t lds)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(g_lds_mu);
+    for (LdsLimit& l : g_lds) {
+        if (l.kern != kern || l.dev != dev) continue;
+        if (l.lds >= lds) return hipSuccess;
+        e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e == hipSuccess) l.lds = lds;
+        return e;
+    }
+    e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e == hipSuccess) g_lds.push_back(LdsLimit{kern, dev, lds});
+    return e;
 }
 
 // Compute units of the current device (queried once per device).

@@ -327,7 +327,7 @@ static hipError_t launch_group_t(const GroupArgs& a, dim3 grid, hipStream_t st)
 {
     const size_t lds = group_lds_bytes(NB);
     auto kern = group_kernel<DT, NB>;
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipError_t e = ensure_lds((const void*)kern, lds);
     if (e != hipSuccess) return e;
     launch(kern, grid, dim3(kMainThreads), lds, st, a);
     return hipGetLastError();

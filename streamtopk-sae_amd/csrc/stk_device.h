@@ -1,7 +1,7 @@
 // stk_device.h -- device-side building blocks for the streaming top-k encoder
-// on gfx950 (CDNA4): sort keys, the MFMA score main loops (MainLoop: W in
-// registers, 4 waves, used by group_kernel; TileStream: W and X staged in
-// LDS, 8 waves, used by main_kernel) and queue compaction helpers.
+// on gfx950 (CDNA4): sort keys, the MFMA quad step, the score main loop
+// (TileStream: W and X staged in LDS, 8 waves, used by main_kernel and
+// group_kernel) and queue compaction helpers.
 //
 // Score layout.  Each wavefront owns blocks of 32 latents (W rows, the MFMA
 // "A" operand) and NB blocks of 32 batch rows (X rows, the MFMA "B" operand),
@@ -16,8 +16,9 @@
 // operands, so every product W[f,d]*X[j,d] is formed exactly once; only the
 // order of the fp32 sum differs from a plain left-to-right dot product.
 //
-// Accumulator layout (checked on the GPU by tests/test_gpu_layout.py):
-// register r of lane l holds row 8*(r/4) + 4*(l/32) + (r%4), column l % 32.
+// Accumulator layout of v_mfma_f32_32x32x*: register r of lane l holds row
+// 8*(r/4) + 4*(l/32) + (r%4), column l % 32 (every GPU parity test depends on
+// it: a wrong map scores the wrong latent).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -100,121 +101,6 @@ __device__ __forceinline__ void mfma_quad<DT_F32>(f32x16& acc, u32x4 a, u32x4 b)
     for (int e = 0; e < 4; ++e)
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[e]), __uint_as_float(b[e]), acc, 0, 0, 0);
 }
-
-// ---------------------------------------------------------------------------
-// Score main loop over d-steps [s_begin, s_end).
-//   wrow[a]  : byte pointer to this lane's W row of block a, already offset by
-//              the lane-half (h * 64 bytes); rows past F are clamped by the
-//              caller to a valid row.
-//   X        : batch rows b0 .. b0 + 32*NB - 1 (rows >= B staged as zeros).
-//   xs0/xs1  : two LDS buffers of 32*NB rows x kXRowStride bytes.
-// The caller's accumulators are added to (not cleared).
-// Ends with a workgroup barrier, so the LDS buffers are free on return.
-// ---------------------------------------------------------------------------
-template <int DT, int NB, int FRAGS>
-struct MainLoop {
-    static constexpr int DS = Dt<DT>::DS;
-    static constexpr int ES = Dt<DT>::esize;
-    static constexpr int kQuadElems = DS / 8;       // elements per 16-byte quad
-    static constexpr int kXChunks = NB;             // 16-byte X chunks per thread per d-step
-
-    const unsigned char* wrow[FRAGS];
-    const unsigned char* X;
-    int64_t B, d, b0;
-    int lane, h;
-
-    __device__ __forceinline__ void load_w(u32x4 (&w)[FRAGS][4], int64_t s) const
-    {
-        const bool full = (s + 1) * DS <= d;
-#pragma unroll
-        for (int a = 0; a < FRAGS; ++a)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int64_t e0 = s * DS + h * (DS / 2) + q * kQuadElems;
-                if (full || e0 < d)
-                    w[a][q] = *(const u32x4*)(wrow[a] + s * kStepBytes + q * 16);
-                else
-                    w[a][q] = u32x4{0u, 0u, 0u, 0u};
-            }
-    }
-
-    __device__ __forceinline__ void load_x(u32x4 (&xr)[kXChunks], int64_t s, int tid) const
-    {
-#pragma unroll
-        for (int p = 0; p < kXChunks; ++p) {
-            const int c = tid + kThreads * p;
-            const int row = c >> 3, c16 = c & 7;
-            const int64_t e0 = s * DS + c16 * kQuadElems;
-            if (b0 + row < B && e0 < d)
-                xr[p] = *(const u32x4*)(X + ((b0 + row) * d + e0) * ES);
-            else
-                xr[p] = u32x4{0u, 0u, 0u, 0u};
-        }
-    }
-
-    __device__ __forceinline__ static void store_x(const u32x4 (&xr)[kXChunks], unsigned char* xs, int tid)
-    {
-#pragma unroll
-        for (int p = 0; p < kXChunks; ++p) {
-            const int c = tid + kThreads * p;
-            const int row = c >> 3, c16 = c & 7;
-            *(u32x4*)(xs + row * kXRowStride + c16 * 16) = xr[p];
-        }
-    }
-
-    __device__ __forceinline__ void compute(f32x16 (&acc)[FRAGS][NB], const u32x4 (&w)[FRAGS][4],
-                                            const unsigned char* xs) const
-    {
-#pragma unroll
-        for (int n = 0; n < NB; ++n)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const u32x4 bx = *(const u32x4*)(xs + (32 * n + (lane & 31)) * kXRowStride + h * 64 + q * 16);
-#pragma unroll
-                for (int a = 0; a < FRAGS; ++a) mfma_quad<DT>(acc[a][n], w[a][q], bx);
-            }
-    }
-
-    // One d-step of the pipeline: publish X(s+1) to LDS, multiply step s,
-    // refill this step's register sets with step s+4, barrier.  Loads are
-    // issued X-then-W per step, so waiting for X(s+1) (issued three steps ago)
-    // leaves the W loads of steps s+2..s+4 in flight.
-#define STK_PIPE_STEP(J, JN, XSC, XSN)                                          \
-    do {                                                                       \
-        const int64_t s = s_begin + base + (J);                               \
-        if (s < s_end) {                                                       \
-            if (s + 1 < s_end) store_x(x##JN, XSN, tid);                      \
-            compute(acc, w##J, XSC);                                           \
-            if (s + 4 < s_end) {                                               \
-                load_x(x##J, s + 4, tid);                                      \
-                load_w(w##J, s + 4);                                           \
-            }                                                                  \
-            __syncthreads();                                                   \
-        }                                                                      \
-    } while (0)
-
-    __device__ __forceinline__ void run(f32x16 (&acc)[FRAGS][NB], int64_t s_begin, int64_t s_end,
-                                        unsigned char* xs0, unsigned char* xs1, int tid) const
-    {
-        if (s_begin >= s_end) return;
-        u32x4 w0[FRAGS][4], w1[FRAGS][4], w2[FRAGS][4], w3[FRAGS][4];
-        u32x4 x0[kXChunks], x1[kXChunks], x2[kXChunks], x3[kXChunks];
-        load_x(x0, s_begin, tid);
-        load_w(w0, s_begin);
-        if (s_begin + 1 < s_end) { load_x(x1, s_begin + 1, tid); load_w(w1, s_begin + 1); }
-        if (s_begin + 2 < s_end) { load_x(x2, s_begin + 2, tid); load_w(w2, s_begin + 2); }
-        if (s_begin + 3 < s_end) { load_x(x3, s_begin + 3, tid); load_w(w3, s_begin + 3); }
-        store_x(x0, xs0, tid);
-        __syncthreads();
-        for (int64_t base = 0; s_begin + base < s_end; base += 4) {
-            STK_PIPE_STEP(0, 1, xs0, xs1);
-            STK_PIPE_STEP(1, 2, xs1, xs0);
-            STK_PIPE_STEP(2, 3, xs0, xs1);
-            STK_PIPE_STEP(3, 0, xs1, xs0);
-        }
-    }
-#undef STK_PIPE_STEP
-};
 
 // ---------------------------------------------------------------------------
 // Compacts the queue segments (in global memory) of this wave's rows that are

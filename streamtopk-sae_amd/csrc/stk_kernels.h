@@ -15,6 +15,11 @@ struct LaunchEvents {
 };
 LaunchEvents& launch_events();
 
+// Raises `kern`'s dynamic-LDS limit to at least `lds` bytes on the current
+// device.  The attribute call is made once per (kernel, device, larger size):
+// later launches only look the pair up.
+hipError_t ensure_lds(const void* kern, size_t lds);
+
 // Every kernel of the library is launched through here.
 template <class K, class... A>
 inline void launch(K kern, dim3 grid, dim3 block, size_t lds, hipStream_t st, A... args)

@@ -707,7 +707,7 @@ static hipError_t launch_main_t(const MainArgs& a, dim3 grid, hipStream_t st)
 {
     const size_t lds = main_lds_bytes(NB, a.cap, a.lq);
     auto kern = main_kernel<DT, NB>;
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipError_t e = ensure_lds((const void*)kern, lds);
     if (e != hipSuccess) return e;
     launch(kern, grid, dim3(kMainThreads), lds, st, a);
     return hipGetLastError();
@@ -729,7 +729,7 @@ static hipError_t launch_sample_t(const SampleArgs& a, dim3 grid, hipStream_t st
 {
     const size_t lds = sample_lds_bytes(NB);
     auto kern = sample_kernel<DT, NB>;
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipError_t e = ensure_lds((const void*)kern, lds);
     if (e != hipSuccess) return e;
     launch(kern, grid, dim3(kSampleThreads), lds, st, a);
     return hipGetLastError();

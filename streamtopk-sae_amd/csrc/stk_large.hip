@@ -576,7 +576,7 @@ static hipError_t launch_mainl_t(const MainLArgs& a, int grid, hipStream_t st)
 {
     const size_t lds = mainl_lds_bytes(a.cap);
     auto kern = mainl_kernel<DT, SAMPLE>;
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipError_t e = ensure_lds((const void*)kern, lds);
     if (e != hipSuccess) return e;
     launch(kern, dim3((unsigned)grid), dim3(kLargeThreads), lds, st, a);
     return hipGetLastError();

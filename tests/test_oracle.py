@@ -81,6 +81,22 @@ def test_exact_ties_and_nan():
     assert I[0].tolist() == [5, 1, 2, 4, 7, 3]
 
 
+@pytest.mark.parametrize("B,F,k", [(3, 50, 1), (5, 300, 17), (2, 1000, 128), (4, 64, 64)])
+def test_topk_scores_matches_bruteforce(B, F, k):
+    """oracle.topk_scores (top-k of given fp32 scores) against a lexsort, with
+    many equal values; NaN ranks first, as torch.topk ranks it."""
+    rng = np.random.default_rng(B * F + k)
+    S = (rng.integers(-40, 40, size=(B, F)) / 3).astype(np.float32)
+    S[0, F // 2] = np.nan
+    V, I = oracle.topk_scores(S, k)
+    key = np.where(np.isnan(S), np.inf, S).astype(np.float64)
+    for i in range(B):
+        want = np.lexsort((np.arange(F), -key[i]))[:k]
+        assert np.array_equal(I[i], want)
+        assert np.array_equal(V[i], S[i, want], equal_nan=True)
+    assert I[0, 0] == F // 2
+
+
 @pytest.mark.parametrize("k", [1, 2, 4, 8, 16, 32, 64, 128])
 def test_buffer_stream_matches_reference_topkbuffer(k):
     """The selection rule restated in stk_oracle_cpu.c vs the reference's own
