@@ -164,7 +164,7 @@ struct ExactPlan {
     int ksplit;                  // d ranges (splits) of the sample pass
     int snb;                     // sample_kernel: 32-row tiles per workgroup
     int64_t list_cap, head_span;
-    size_t off_thr, off_P, off_list, off_lcnt, off_seg, off_queue, total;
+    size_t off_thr, off_list, off_lcnt, off_seg, total;
 };
 
 static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int dtype, int ncu)
@@ -188,8 +188,6 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
         const int64_t bblocks = cdiv(B > 0 ? B : 1, 32);
         p.NB = (int)(bblocks < 4 ? bblocks : 4);
         if (p.NB == 3) p.NB = 4;
-        p.lq = main_lds_queue(p.NB, (int)k);
-        p.cap = (int)((k + p.lq + 1) & ~(int64_t)1);
         p.nbc = cdiv(B, 32 * p.NB);
         int64_t nwg = ncu / (p.nbc > 0 ? p.nbc : 1);
         if (nwg < 1) nwg = 1;
@@ -231,22 +229,46 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
         if (ks < cdiv(nds, kSampleSteps)) ks = cdiv(nds, kSampleSteps);
         p.ksplit = (int)ks;
     }
-    p.head_span = p.sample ? p.nsamp : 0;
-    // main_kernel: a workgroup leaves up to cap segment keys and lq queue keys per row
-    p.list_cap = p.head_span + (int64_t)p.nwg * (p.large ? p.cap : p.cap + p.lq);
+    if (!p.large) {
+        // main_kernel's LDS queue: room for about twice the survivors a
+        // workgroup expects per row (the scores above the sample's k-th,
+        // k * F / nsamp per row, spread over the workgroups), up to what fits
+        // next to its rings; without a sample every score passes at first and
+        // the queue takes all the room there is.
+        const int lq_max = main_lds_queue(p.NB, (int)k);
+        int lq = lq_max;
+        if (p.sample) {
+            const int64_t expect = cdiv(k * F / p.nsamp, p.nwg);
+            const int64_t want = (2 * expect + 8 + 1) & ~(int64_t)1;
+            if (want < lq) lq = (int)want;
+        }
+        p.lq = lq;
+        p.cap = (int)((k + p.lq + 1) & ~(int64_t)1);
+    }
+    // Each row's list: a head (the sample's top k; with a sample larger than
+    // the selection buffer, every sampled key that reaches its first bound),
+    // then one segment of cap keys per workgroup of the streaming kernel.
+    // The sample pass's partial sums of the row live in the segment area:
+    // they are dead (read by thr_kernel) before the first segment is written.
+    if (!p.sample)
+        p.head_span = 0;
+    else if (p.nsamp <= kSelCap)
+        p.head_span = (k + 1) & ~(int64_t)1;
+    else
+        p.head_span = p.nsamp;
+    int64_t seg_keys = (int64_t)p.nwg * p.cap;
+    const int64_t p_keys = p.sample ? ((int64_t)p.ksplit * p.nsamp + 1) / 2 : 0;
+    if (p_keys > seg_keys) seg_keys = p_keys;
+    p.list_cap = (p.head_span + seg_keys + 1) & ~(int64_t)1;
     size_t off = 0;
     p.off_thr = off;
     off = align256(off + (size_t)B * 8);
-    p.off_P = off;
-    if (p.sample) off = align256(off + (size_t)p.ksplit * B * p.nsamp * 4);
-    p.off_list = off;
-    off = align256(off + (size_t)B * p.list_cap * 8);
     p.off_lcnt = off;
     off = align256(off + (size_t)B * 4 * kCntStride);
     p.off_seg = off;
-    if (p.large) off = align256(off + (size_t)B * p.nwg * 4);
-    p.off_queue = off;   // main_kernel: each workgroup's row queues
-    if (!p.large) off = align256(off + (size_t)p.nbc * p.nwg * 32 * p.NB * p.cap * 8);
+    off = align256(off + (size_t)B * p.nwg * 4);
+    p.off_list = off;
+    off = align256(off + (size_t)B * p.list_cap * 8);
     p.total = off;
     return p;
 }
@@ -303,7 +325,10 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     uint64_t* thr = (uint64_t*)(ws + p.off_thr);
     uint64_t* list_keys = (uint64_t*)(ws + p.off_list);
     int32_t* list_cnt = (int32_t*)(ws + p.off_lcnt);
-    float* P = p.sample ? (float*)(ws + p.off_P) : nullptr;
+    int32_t* seg_cnt = (int32_t*)(ws + p.off_seg);
+    // the sample's partial sums: in each row's segment area, split after split
+    float* P = p.sample ? (float*)(list_keys + p.head_span) : nullptr;
+    const int64_t p_row = 2 * p.list_cap, p_split = p.nsamp;
     if (p.sample && p.large) {
         MainLArgs sl;
         std::memset(&sl, 0, sizeof sl);
@@ -314,6 +339,8 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         sl.ksplit = p.ksplit;
         sl.nsamp = p.nsamp;
         sl.P = P;
+        sl.p_row = p_row;
+        sl.p_split = p_split;
         const int grid = (int)(p.nbc * (p.nsamp / kTileLatents) * p.ksplit);
         int pi = prof_begin("sample_kernel", st);
         e = launch_mainl_sample(dt, sl, grid, st);
@@ -326,6 +353,8 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         sa.nsamp = p.nsamp;
         sa.nsplit = p.ksplit;
         sa.P = P;
+        sa.p_row = p_row;
+        sa.p_split = p_split;
         const dim3 grid((unsigned)(p.nsamp / kSampleLat * p.ksplit), (unsigned)cdiv(B, 32 * p.snb));
         int pi = prof_begin("sample_kernel", st);
         e = launch_sample(dt, p.snb, sa, grid, st);
@@ -334,6 +363,8 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     }
     ThrArgs ta;
     ta.P = P;
+    ta.p_row = p_row;
+    ta.p_split = p_split;
     ta.nsplit = p.ksplit;
     ta.bias = b;
     ta.samp_log2 = p.samp_log2; ta.nsamp = p.nsamp; ta.k = (int)k;
@@ -355,7 +386,7 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         ml.samp_log2 = p.samp_log2;
         ml.samp_blocks = p.nsamp / kSampleBlock;
         ml.list_keys = list_keys; ml.list_cap = p.list_cap; ml.head_span = p.head_span;
-        ml.seg_cnt = (int32_t*)(ws + p.off_seg);
+        ml.seg_cnt = seg_cnt;
         int pm = prof_begin("main_kernel", st);
         e = launch_mainl(dt, ml, (int)(p.nbc * p.nwg), st);
         prof_end(pm, st);
@@ -372,18 +403,21 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         ma.sampled = p.sample ? 1 : 0;
         ma.samp_log2 = p.samp_log2;
         ma.samp_blocks = p.nsamp / kSampleBlock;
-        ma.list_keys = list_keys; ma.list_cnt = list_cnt; ma.list_cap = p.list_cap;
-        ma.queue = (uint64_t*)(ws + p.off_queue);
+        ma.list_keys = list_keys; ma.list_cap = p.list_cap; ma.head_span = p.head_span;
+        ma.seg_cnt = seg_cnt;
         ma.lq = p.lq;
         int pm = prof_begin("main_kernel", st);
         e = launch_main(dt, p.NB, ma, dim3((unsigned)p.nwg, (unsigned)p.nbc), st);
         prof_end(pm, st);
         if (e != hipSuccess) return hip_fail(e, "main_kernel launch");
         mg.list_keys = list_keys; mg.list_cnt = list_cnt; mg.list_cap = p.list_cap;
-        mg.head_span = p.list_cap; mg.nseg = 0; mg.seg_cap = 1; mg.seg_cnt = nullptr;
-        // a sampled row keeps about k + k * F / nsamp candidates (the scores
-        // at or above the sample's k-th)
-        mg.spec = (p.sample && k + k * F / p.nsamp > 4096) ? 1 : 0;
+        mg.head_span = p.head_span; mg.nseg = p.nwg; mg.seg_cap = p.cap; mg.seg_cnt = seg_cnt;
+        // the head holds at most k keys (nsamp <= kSelCap): one segment per
+        // merge thread, read in place, in passes of 30 keys where a segment
+        // expects at most ~12 (k * F / nsamp keys per row over the
+        // workgroups), else of 62
+        const int64_t per_seg = p.sample ? cdiv(k * F / p.nsamp, p.nwg) : p.cap;
+        mg.spec = per_seg <= 12 ? 3 : 4;
     }
     mg.k = (int)k;
     mg.f_offset = (int32_t)f_offset;
@@ -593,6 +627,9 @@ int stk_approx_forward(const void* X, const void* W, const float* b, float* V, i
     if ((rc = check_ptrs(X, W, b, V, I))) return rc;
     if ((cand_vals == nullptr) != (cand_idxs == nullptr))
         return set_error(STK_E_INVALID, "cand_vals and cand_idxs must both be given or both be NULL");
+    // group_kernel writes each group's candidates as 16-byte vectors
+    if (((uintptr_t)cand_vals | (uintptr_t)cand_idxs) & 15)
+        return set_error(STK_E_INVALID, "cand_vals and cand_idxs must be 16-byte aligned");
     int ncu = 0;
     if ((rc = cu_count(&ncu))) return rc;
     hipStream_t st = (hipStream_t)stream;

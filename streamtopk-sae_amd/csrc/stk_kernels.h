@@ -71,17 +71,14 @@ struct MainArgs {
     const uint64_t* thr0;        // per-row starting threshold keys, or null
     int sampled;                 // non-zero: the sampled latents (is_sampled) were
     int samp_log2, samp_blocks;  //   scored by the sample pass and are skipped here
-    uint64_t* list_keys;         // [B][list_cap]: every workgroup's final queue, appended
-    int32_t* list_cnt;           // [B * kCntStride] keys in each row's list (set by thr_kernel)
-    int64_t list_cap;            // nsamp + nwg * (cap + lq): room for the sampled
-                                 //   keys and every workgroup's keys
-    uint64_t* queue;             // [nbc][nwg][32*NB][cap] each workgroup's row segments
+    uint64_t* list_keys;         // [B][list_cap]: row r's head (head_span slots, the
+    int64_t list_cap, head_span; //   sample's top k), then one segment of cap keys
+                                 //   per workgroup (gridDim.x of them)
+    int32_t* seg_cnt;            // [B][gridDim.x] keys each workgroup left in its segment
     int lq;                      // LDS queue keys per row (even, <= 64; cap >= k + lq)
 };
 
-// Row r's candidate count is list_cnt[r * kCntStride]: one 128-byte line per
-// row, so that the workgroups' end-of-kernel atomics on different rows do not
-// queue on the same L2 line.
+// Row r's head count is list_cnt[r * kCntStride]: one 128-byte line per row.
 constexpr int kCntStride = 32;
 
 constexpr int kSampleWaves = 8;      // wavefronts per sample_kernel workgroup
@@ -95,12 +92,13 @@ struct SampleArgs {
     int64_t B, d;
     int samp_log2, nsamp;
     int nsplit;                  // d ranges (splits) of the sample pass
-    float* P;                    // [nsplit][B][nsamp] partial scores of the sampled latents
+    float* P;                    // partial scores of the sampled latents: split s,
+    int64_t p_row, p_split;      //   row j, sample i at P[j * p_row + s * p_split + i]
 };
 
 struct ThrArgs {
     const float* P;              // sampled scores, or null (no sample: threshold 0):
-                                 //   nsplit partial sums [nsplit][B][nsamp]
+    int64_t p_row, p_split;      //   nsplit partial sums (layout as in SampleArgs)
     int nsplit;                  //   added in split order, then
     const float* bias;           //   + bias[latent] if non-null
     int samp_log2, nsamp, k;
@@ -132,7 +130,8 @@ struct MainLArgs {
     // sample mode (mainl_sample_kernel): 256-latent tiles of the sampled
     // latents, d split in ksplit ranges; raw partial scores to P
     int ksplit, nsamp;
-    float* P;                    // [ksplit][B][nsamp]
+    float* P;                    // split s, row j, sample i at P[j * p_row + s * p_split + i]
+    int64_t p_row, p_split;
 };
 
 // A row's candidates: slots [0, head_span) hold list_cnt[row * kCntStride] keys at their
@@ -148,8 +147,11 @@ struct MergeArgs {
     int nseg, seg_cap;
     const int32_t* seg_cnt;      // [B][nseg]
     int k;
-    int spec;                    // non-zero: a dense list expected to hold more than
-                                 //   4096 candidates (one-chunk variant)
+    int spec;                    // 0: chunks of 16 candidates per thread; a list
+                                 //   expected to hold more than 4096 candidates
+                                 //   (32 per thread and chunk): 1 dense, 2 segmented;
+                                 //   3, 4: merge_seg_kernel (head <= 256 keys, one
+                                 //   segment per thread; 30 or 62 keys per pass)
     int32_t f_offset;            // added to every emitted index (a shard's first latent)
     float* V;
     int32_t* I;

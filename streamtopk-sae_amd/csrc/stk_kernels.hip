@@ -10,10 +10,11 @@
 //                    rows per tile (the sampled latents are skipped: each latent
 //                    is scored by exactly one kernel); scores not below the
 //                    row threshold go to a short per-row LDS queue, which
-//                    spills to a per-row global segment when it fills; a full
-//                    segment is rank-compacted to its top-k.  Appends each
-//                    workgroup's keys to a dense per-row candidate list.
-//   merge_kernel   : per row, top-k of its candidate list.
+//                    spills to the workgroup's segment of the row's list when
+//                    it fills; a full segment is rank-compacted to its top-k.
+//                    At the end every queue is flushed to its segment.
+//   merge_seg_kernel / merge_kernel : per row, top-k of its candidate list
+//                    (the head and one segment per workgroup).
 //
 // The reference's pass 1 / pass 2 split (streamtopk_exact.cu:58-187 tile
 // kernel, :429-499 merge kernel) maps to main_kernel / merge_kernel; its
@@ -49,31 +50,35 @@ __device__ __forceinline__ float pick16(const f32x16& v, uint32_t r)
 // ---------------------------------------------------------------------------
 // main_kernel
 // ---------------------------------------------------------------------------
-// Spills the full LDS queues among this wave's rows (wave*R .. wave*R+R-1)
-// to their global segments: a segment without room for a whole LDS queue is
-// first rank-compacted to its top k (raising the row threshold), then the
-// LDS keys above the threshold are appended.  Every global access of a row is
-// made by the wave that owns the row.  Ends with the wave's stores complete.
+// Spills LDS queues among this wave's rows (wave*R .. wave*R+R-1) to their
+// global segments (row r's at seg + r * seg_stride, cap keys): the full ones,
+// or with `all` every non-empty one.  A segment without room for the queue's
+// keys is first rank-compacted to its top k (raising the row threshold), then
+// the LDS keys above the threshold are appended.  Every global access of a
+// row is made by the wave that owns the row.  Ends with the wave's stores
+// complete.
 template <int R>
-__device__ __forceinline__ void spill_full_rows(int* cnt, int* gcnt, uint64_t* thr, const uint64_t* lqk,
-                                                uint64_t* seg, uint64_t* scr, int lq, int cap, int k, int wave,
-                                                int lane)
+__device__ __forceinline__ void spill_rows(int* cnt, int* gcnt, uint64_t* thr, const uint64_t* lqk,
+                                           uint64_t* seg, int64_t seg_stride, uint64_t* scr, int lq, int cap,
+                                           int k, int wave, int lane, bool all)
 {
     const int myrow = wave * R + (lane < R ? lane : 0);
-    uint64_t full = __ballot(lane < R && cnt[myrow] >= lq);
+    const int mycnt = cnt[myrow];
+    uint64_t full = __ballot(lane < R && (all ? mycnt > 0 : mycnt >= lq));
     while (full) {
         const int i = __builtin_ctzll(full);
         full &= full - 1;
         const int row = wave * R + i;
-        uint64_t* q = seg + (size_t)row * cap;
+        uint64_t* q = seg + row * seg_stride;
+        const int nl = cnt[row] < lq ? cnt[row] : lq;
         int g = gcnt[row];
         uint64_t t = thr[row];
-        if (g + lq > cap) {
+        if (g + nl > cap) {
             t = compact_row(q, g, scr, cap, k, lane);
             g = k;
         }
         // lq <= 64: one key per lane
-        const uint64_t key = lane < lq ? lqk[row * lq + lane] : 0ull;
+        const uint64_t key = lane < nl ? lqk[row * lq + lane] : 0ull;
         const bool f = key > t;
         const uint64_t bal = __ballot(f);
         const int pos = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
@@ -110,8 +115,9 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
     const int64_t b0 = (int64_t)blockIdx.y * BT;
     const int64_t B = a.B, F = a.F;
     const int k = a.k;
-    // this workgroup's global segments: cap keys per row
-    uint64_t* seg = a.queue + ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * BT * cap;
+    // this workgroup's global segments: cap keys in each row's list (row
+    // b0 + r at seg + r * list_cap; rows past B are never written)
+    uint64_t* seg = a.list_keys + b0 * a.list_cap + a.head_span + (int64_t)blockIdx.x * cap;
 
     for (int i = tid; i < BT; i += kMainThreads) {
         thr[i] = (a.thr0 != nullptr && b0 + i < B) ? a.thr0[b0 + i] : 0ull;
@@ -208,7 +214,7 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
             }
             if (!__syncthreads_or(overflow)) break;
             __syncthreads();   // the LDS queues are complete
-            spill_full_rows<R>(cnt, gcnt, thr, lqk, seg, cscr + wave * cap, lq, cap, k, wave, lane);
+            spill_rows<R>(cnt, gcnt, thr, lqk, seg, a.list_cap, cscr + wave * cap, lq, cap, k, wave, lane, false);
             __syncthreads();
             // drop pending scores that fell below a raised threshold
 #pragma unroll
@@ -224,23 +230,13 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
         }
     });
 
-    // ---- append this workgroup's keys to the rows' candidate lists: each
-    // wave its R rows, the global segment's keys then the LDS queue's ----
+    // ---- flush: every wave moves its R rows' LDS queues into their global
+    // segments (compacting a segment without room), then publishes how many
+    // keys each of its segments holds ----
     __syncthreads();
-    const int myrow = wave * R + (lane < R ? lane : 0);
-    const bool own = lane < R && b0 + myrow < B;
-    const int nl = own ? (cnt[myrow] < lq ? cnt[myrow] : lq) : 0;
-    const int ng = own ? gcnt[myrow] : 0;
-    const int lbase = (nl + ng) ? atomicAdd(&a.list_cnt[(b0 + myrow) * kCntStride], nl + ng) : 0;
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-        const int rl = __shfl(nl, i, 64), rg = __shfl(ng, i, 64), rb = __shfl(lbase, i, 64);
-        const int row = wave * R + i;
-        uint64_t* dst = a.list_keys + (size_t)(b0 + row) * a.list_cap + rb;
-        const uint64_t* q = seg + (size_t)row * cap;
-        for (int e = lane; e < rg; e += 64) dst[e] = __hip_atomic_load(q + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (lane < rl) dst[rg + lane] = lqk[row * lq + lane];
-    }
+    spill_rows<R>(cnt, gcnt, thr, lqk, seg, a.list_cap, cscr + wave * cap, lq, cap, k, wave, lane, true);
+    const int myrow = wave * R + lane;
+    if (lane < R && b0 + myrow < B) a.seg_cnt[(b0 + myrow) * gridDim.x + blockIdx.x] = gcnt[myrow];
 }
 
 // ---------------------------------------------------------------------------
@@ -355,7 +351,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a)
             *(f32x4*)(T + (sl * BT + 32 * n + jl) * kSampleStride + 32 * g + 8 * e + 4 * h) =
                 f32x4{acc[n][4 * e], acc[n][4 * e + 1], acc[n][4 * e + 2], acc[n][4 * e + 3]};
     __syncthreads();
-    float* Ps = a.P + (int64_t)sp * a.B * a.nsamp;
+    float* Ps = a.P + (int64_t)sp * a.p_split;
     constexpr int WS = BT * kSampleStride;
     for (int c = tid; c < BT * 16; c += kSampleThreads) {
         const int row = c >> 4, c4 = (c & 15) * 4;
@@ -364,7 +360,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a)
             const float* t0 = T + row * kSampleStride + c4;
             const f32x4 v = ((*(const f32x4*)t0 + *(const f32x4*)(t0 + WS)) + *(const f32x4*)(t0 + 2 * WS)) +
                             *(const f32x4*)(t0 + 3 * WS);
-            *(f32x4*)(Ps + j * a.nsamp + ib + c4) = v;
+            *(f32x4*)(Ps + j * a.p_row + ib + c4) = v;
         }
     }
 }
@@ -391,8 +387,8 @@ __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
     // four consecutive sampled latents (one 16-byte load of P) per quad
     constexpr int kQuads = kItems / 4;
     auto item = [&](int t) { return 4 * tid + kThreads * 4 * (t >> 2) + (t & 3); };
-    const float* prow = a.P + row * (kItems * kThreads);
-    const int64_t split_stride = (int64_t)gridDim.x * (kItems * kThreads);   // B rows per split
+    const float* prow = a.P + row * a.p_row;
+    const int64_t split_stride = a.p_split;
     f32x4 v[kQuads];
 #pragma unroll
     for (int u = 0; u < kQuads; ++u) v[u] = *(const f32x4*)(prow + item(4 * u));
@@ -439,14 +435,14 @@ __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
         __syncthreads();
         T = S.thr;
     } else if (n <= kSelCap) {
-        for (int i0 = 0; i0 < n; i0 += kThreads) {
-            const int i = i0 + tid;
-            const uint64_t kk = i < n ? S.buf[i] : 0ull;
-            const bool f = i < n && kk >= T;
-            const int pos = wave_reserve1(&S.sel_cnt, f);
-            if (f) out[pos] = kk;
-        }
+        // the sample's k largest keys (unordered): the k-th is the threshold
+        select_compact(S, n, a.k, tid);
+        if (tid < a.k) out[tid] = S.buf[tid];
+        if (tid == 0) S.sel_cnt = a.k;
+        T = S.thr;
     } else {
+        // (only a sample larger than the selection buffer gets here: the head
+        // then holds every sampled key that reaches T0, up to nsamp)
         uint32_t hit = 0;
 #pragma unroll
         for (int t = 0; t < kItems; ++t) hit |= (key[t] >= T) ? (1u << t) : 0u;
@@ -459,6 +455,52 @@ __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
     if (tid == 0) {
         a.thr[row] = T;
         a.list_cnt[row * kCntStride] = S.sel_cnt;
+    }
+}
+
+// One pass of the per-row selection: every thread holds N keys in v (0 for
+// none).  The keys that reach the larger of the pass's bound (the k-th of the
+// per-thread maxima: k of the pass's keys reach it) and `run` (the k-th key of
+// the last compaction) go to S.buf; when it fills, it is compacted to its top
+// k, which raises `run`.  Every thread of the workgroup takes part.
+template <int N>
+__device__ __forceinline__ void merge_pass(SelShared& S, const uint64_t (&v)[N], int k, int tid, uint64_t& run)
+{
+    static_assert(N <= 64, "pending mask");
+    using Mask = std::conditional_t<(N > 32), uint64_t, uint32_t>;
+    constexpr Mask one = 1;
+    uint64_t m = 0;
+#pragma unroll
+    for (int u = 0; u < N; ++u) m = v[u] > m ? v[u] : m;
+    const uint64_t T = kth_of_maxima(S, m, k, tid);
+    const uint64_t thr = T > run ? T : run;
+    Mask pend = 0;
+#pragma unroll
+    for (int u = 0; u < N; ++u) pend |= (v[u] != 0 && v[u] >= thr) ? (one << u) : Mask(0);
+    for (;;) {
+        bool stalled = false;
+        const Mask pm = pend;
+        const int base = wave_reserve(&S.cnt, __popcll((uint64_t)pm));
+#pragma unroll
+        for (int u = 0; u < N; ++u) {
+            if (pm >> u & one) {
+                const int pos = base + __popcll((uint64_t)(pm & ((one << u) - one)));
+                if (pos < kSelCap) {
+                    S.buf[pos] = v[u];
+                    pend &= ~(one << u);
+                } else {
+                    stalled = true;
+                }
+            }
+        }
+        if (!__syncthreads_or(stalled)) break;
+        select_compact(S, kSelCap, k, tid);   // S.cnt = k, S.thr = k-th key
+        const uint64_t r2 = S.thr;
+        run = r2;
+        Mask keep = 0;
+#pragma unroll
+        for (int u = 0; u < N; ++u) keep |= (v[u] > r2) ? (one << u) : Mask(0);
+        pend &= keep;
     }
 }
 
@@ -517,7 +559,6 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
     }
     uint64_t run = 0;
     for (int64_t c0 = 0; c0 < n; c0 += (int64_t)kPer * kThreads) {
-        uint64_t m = 0;
         if (nseg > 0) {
             // segment of each segment candidate: the number of segments whose
             // inclusive prefix is <= its index (all items searched in step)
@@ -558,35 +599,67 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
                     v[u] = ok ? keys[i] : 0ull;
             }
         }
+        merge_pass(S, v, k, tid, run);
+    }
+    emit_topk(S, k, tid, [&](int r, uint64_t kk) {
+        a.V[row * k + r] = key_value(kk);
+        a.I[row * k + r] = key_index(kk) + a.f_offset;
+    });
+}
+
+// Per row: top-k of main_kernel's list -- a head of at most kThreads keys,
+// then nseg segments of seg_cap slots, segment s holding seg_cnt[row * nseg +
+// s] keys.  Thread t reads head key t and the keys of segments t, t +
+// kThreads, ..., kPer consecutive keys per pass (16-byte loads): no search for
+// a key's segment, and every thread has its loads in flight at once.  The
+// head key and the first kEager keys of a segment (one 128-byte line) are
+// loaded without waiting for the counts and masked afterwards.  A pass filters
+// as merge_kernel's chunks.
+template <int kPer, int kEager>
+__global__ __launch_bounds__(kThreads) void merge_seg_kernel(MergeArgs a)
+{
+    static_assert(kPer % 2 == 0 && kEager % 2 == 0 && kEager <= kPer, "pairs of keys");
+    __shared__ SelShared S;
+    const int tid = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    const int k = a.k;
+    const int nseg = a.nseg;
+    const int64_t hs = a.head_span;   // <= kThreads (host)
+    const uint64_t* keys = a.list_keys + row * a.list_cap;
+    uint64_t v[kPer + 1];
+    v[kPer] = tid < hs ? keys[tid] : 0ull;   // the head key rides in the first pass
+    const int hc = a.list_cnt[row * kCntStride];
+    if (tid == 0) S.cnt = 0;
+    uint64_t run = 0;
+    for (int s0 = 0; s0 < nseg || s0 == 0; s0 += kThreads) {
+        const int sg = s0 + tid;
+        const bool own = sg < nseg;
+        // segment starts are 16-byte aligned (head_span and seg_cap even)
+        const uint64_t* q = keys + hs + (int64_t)(own ? sg : 0) * a.seg_cap;
+        u64x2 e[kEager / 2];
 #pragma unroll
-        for (int u = 0; u < kPer; ++u) m = v[u] > m ? v[u] : m;
-        const uint64_t T = kth_of_maxima(S, m, k, tid);
-        const uint64_t thr = T > run ? T : run;
-        uint32_t pend = 0;
+        for (int u = 0; u < kEager; u += 2) {
+            e[u / 2] = u64x2{0ull, 0ull};
+            if (own && u < a.seg_cap) e[u / 2] = *(const u64x2*)(q + u);
+        }
+        const int cnt = own ? a.seg_cnt[row * nseg + sg] : 0;
+        if (s0 == 0 && tid >= hc) v[kPer] = 0ull;
+        for (int base = 0;; base += kPer) {
 #pragma unroll
-        for (int u = 0; u < kPer; ++u) pend |= (v[u] != 0 && v[u] >= thr) ? (1u << u) : 0u;
-        for (;;) {
-            bool stalled = false;
-            const uint32_t pm = pend;
-            const int base = wave_reserve(&S.cnt, __builtin_popcount(pm));
-#pragma unroll
-            for (int u = 0; u < kPer; ++u) {
-                if (pm >> u & 1u) {
-                    const int pos = base + __builtin_popcount(pm & ((1u << u) - 1u));
-                    if (pos < kSelCap) {
-                        S.buf[pos] = v[u];
-                        pend &= ~(1u << u);
-                    } else {
-                        stalled = true;
-                    }
-                }
+            for (int u = 0; u < kPer; u += 2) {
+                // a pair starting below the count lies inside the segment
+                // (cnt <= seg_cap, both even)
+                u64x2 p = {0ull, 0ull};
+                if (u < kEager && base == 0)
+                    p = e[u / 2];
+                else if (base + u < cnt)
+                    p = *(const u64x2*)(q + base + u);
+                v[u] = base + u < cnt ? p[0] : 0ull;
+                v[u + 1] = base + u + 1 < cnt ? p[1] : 0ull;
             }
-            if (!__syncthreads_or(stalled)) break;
-            select_compact(S, kSelCap, k, tid);   // S.cnt = k, S.thr = k-th key
-            run = S.thr;
-#pragma unroll
-            for (int u = 0; u < kPer; ++u)
-                if ((pend >> u & 1u) && !(v[u] > run)) pend &= ~(1u << u);
+            merge_pass(S, v, k, tid, run);
+            v[kPer] = 0ull;
+            if (!__syncthreads_or(cnt > base + kPer)) break;
         }
     }
     emit_topk(S, k, tid, [&](int r, uint64_t kk) {
@@ -771,12 +844,18 @@ hipError_t launch_pack(const PackArgs& a, int64_t rows, hipStream_t st)
 
 hipError_t launch_merge(const MergeArgs& a, int64_t rows, hipStream_t st)
 {
-    // dense lists expected to exceed one 4096-slot chunk: 32 slots per thread
-    // (one chunk), the first 16 loaded ahead of the count; otherwise 16 slots
-    // per thread, which also keeps the registers low enough for four
-    // workgroups per CU when the rows are many (large batches)
-    if (a.spec > 0)
+    // lists expected to exceed one 4096-slot chunk: 32 slots per thread (one
+    // chunk); a dense one (spec 1) has its first 16 loaded ahead of the count;
+    // otherwise 16 slots per thread, which also keeps the registers low enough
+    // for four workgroups per CU when the rows are many (large batches)
+    if (a.spec == 1)
         launch(merge_kernel<32, 16>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+    else if (a.spec == 2)
+        launch(merge_kernel<32, 0>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+    else if (a.spec == 3)   // segments expected to hold up to ~12 keys: 30 per pass
+        launch(merge_seg_kernel<30, 16>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+    else if (a.spec == 4)   // fuller segments: 62 per pass, so that one pass covers them
+        launch(merge_seg_kernel<62, 16>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     else
         launch(merge_kernel<16, 0>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     return hipGetLastError();

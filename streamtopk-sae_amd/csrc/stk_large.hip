@@ -387,8 +387,8 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
             __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0)
             __syncthreads();
             if (SAMPLE) {
-                // raw partial scores of this d range: P[ks][row][sample index]
-                float* P = a.P + (int64_t)ks * B * a.nsamp;
+                // raw partial scores of this d range (split ks)
+                float* P = a.P + (int64_t)ks * a.p_split;
 #pragma unroll
                 for (int n = 0; n < kLNB; ++n) {
                     const int64_t row = b0 + rw0 + 32 * n + jl;
@@ -401,7 +401,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                                 f32x4 v;
 #pragma unroll
                                 for (int e = 0; e < 4; ++e) v[e] = acc[fa][n][r4 * 4 + e];
-                                *(f32x4*)(P + row * a.nsamp + i) = v;
+                                *(f32x4*)(P + row * a.p_row + i) = v;
                             }
                     }
                 }

@@ -229,6 +229,7 @@ def approx_forward(X, W_enc, b_enc, k, c, candidate_buffer=None, candidates=Fals
     with torch.cuda.device(X.device):
         with_cand = candidate_buffer is not None or candidates
         cand_vals = cand_idxs = None
+        copy_back = None
         if with_cand:
             if candidate_buffer is not None:
                 cb = candidate_buffer
@@ -236,6 +237,10 @@ def approx_forward(X, W_enc, b_enc, k, c, candidate_buffer=None, candidates=Fals
                     raise RuntimeError("candidate_buffer shape mismatch")
                 if cb.dtype != torch.float32 or cb.device != X.device or not cb.is_contiguous():
                     raise RuntimeError("candidate_buffer must be a contiguous fp32 tensor on X's device")
+                if cb.data_ptr() % 16:
+                    # the kernel writes 16-byte vectors: fill an aligned buffer, then copy
+                    copy_back = cb
+                    cb = torch.empty_like(cb)
                 cand_vals = cb
             else:
                 cand_vals = torch.empty((B, nt, c), dtype=torch.float32, device=X.device)
@@ -251,6 +256,9 @@ def approx_forward(X, W_enc, b_enc, k, c, candidate_buffer=None, candidates=Fals
                                     B, d, F, k, c, dt, _ptr(cand_vals), _ptr(cand_idxs),
                                     _ptr(ws), ws.numel(), ctypes.c_void_p(stream))
         _lib.check(rc)
+        if copy_back is not None:
+            copy_back.copy_(cand_vals)
+            cand_vals = copy_back
     return V, I, cand_vals, cand_idxs
 
 

@@ -66,6 +66,21 @@ def test_approx_argument_errors(k, c, msg):
     assert msg in lib.stk_last_error().decode()
 
 
+def test_approx_candidate_pointer_checks():
+    """Candidate buffers are written as 16-byte vectors: a misaligned pointer,
+    or only one of the two, is rejected before any device work (the pointers
+    here are never dereferenced)."""
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x10000)
+    for cv, ci, msg in [(ctypes.c_void_p(0x10004), fake, "must be 16-byte aligned"),
+                        (fake, ctypes.c_void_p(0x10008), "must be 16-byte aligned"),
+                        (fake, None, "must both be given or both be NULL")]:
+        rc = lib.stk_approx_forward(fake, fake, fake, fake, fake, 4, 64, 256, 8, 16, 2,
+                                    cv, ci, None, 0, None)
+        assert rc == 1
+        assert msg in lib.stk_last_error().decode()
+
+
 def test_cpu_forward_through_abi():
     import oracle
     lib = _lib.load()

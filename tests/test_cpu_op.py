@@ -29,6 +29,19 @@ def test_cpu_op_vs_oracle(B, d, F, k):
     check_against_scores(V.numpy(), I.numpy(), S, k, 1e-5, "cpu op")
 
 
+def test_cpu_op_config0_shape():
+    """BASELINE config 0 at its own shape and inputs (fp32 B=32 d=768 F=16384
+    k=32, the seeded generator of the benchmark) against the oracle at the
+    fp32 tolerance (reference tests/test_correctness.py:127-152)."""
+    from streamtopk_sae import make_inputs
+    X, W, b = make_inputs(32, 768, 16384, torch.float32, seed=0, device="cpu")
+    V, I = topk_sae_cpu(X, W, b, 32)
+    S = oracle.scores_f64(X.numpy(), W.numpy(), b.numpy())
+    check_against_scores(V.numpy(), I.numpy(), S, 32, 1e-5, "cpu config0")
+    Vo, Io = oracle.exact(X.numpy(), W.numpy(), b.numpy(), 32, nthreads=4)
+    assert np.abs(V.numpy() - Vo).max() <= 1e-5 * max(1.0, float(np.abs(Vo).max()))
+
+
 @pytest.mark.parametrize("k", [16, 32, 64])
 def test_cpu_op_k(k):
     X, W, b = _inputs(16, 128, 512, k)
