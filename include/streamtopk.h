@@ -64,6 +64,25 @@ int stk_exact_forward(const void* X, const void* W, const float* b, float* V, in
                       int64_t B, int64_t d, int64_t F, int64_t k, int dtype,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of the static device scratch stk_exact_forward_noalloc works in. */
+#define STK_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* stk_exact_forward without a workspace, for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc.  No counterpart in the reference.  The workspace is
+ * a static device array of STK_NOALLOC_SCRATCH_BYTES in the library's code
+ * object, held by every device that runs this entry point until the process
+ * ends; the call allocates nothing and records no profiling events.  A
+ * problem whose stk_exact_workspace_bytes exceeds the array is rejected with
+ * STK_E_WORKSPACE before any device work: batches of up to 256 rows fit for
+ * any d <= 4096, k <= 128 and F (BASELINE configs 1-3 need 12-28 MB);
+ * batches of 512 rows and more (config 4) do not.  All calls on one device
+ * share its array, so calls that overlap on one device race: serialise them
+ * (one stream, or events between streams).  Results are identical to
+ * stk_exact_forward's. */
+int stk_exact_forward_noalloc(const void* X, const void* W, const float* b, float* V, int32_t* I,
+                              int64_t B, int64_t d, int64_t F, int64_t k, int dtype, void* stream);
+
 /* Exact encode of one shard of W: W and b hold latents f_offset ..
  * f_offset + F - 1 of a larger dictionary, and I receives those global
  * indices (local index + f_offset).  Otherwise identical to

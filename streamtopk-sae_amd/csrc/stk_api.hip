@@ -468,6 +468,42 @@ static int validate_approx(int64_t B, int64_t d, int64_t F, int64_t k, int64_t c
     return 0;
 }
 
+// ---------------------------------------------------------------------------
+// Static scratch of stk_exact_forward_noalloc
+// ---------------------------------------------------------------------------
+// The exact path's workspace for callers that cannot allocate: a file-scope
+// array in the code object, so every device that runs the entry point holds
+// its own copy until the process ends.  In host code `scratch` names a
+// host-side stand-in, not a device address: each device's address comes from
+// hipGetSymbolAddress, resolved once per device with that device current,
+// and only that address is handed to kernels.  Nothing in it needs to start
+// at zero: every count and key a kernel reads is written earlier in the same
+// call (thr_kernel writes each row's threshold and head count, main_kernel
+// every segment count).
+__attribute__((used)) static __device__ __align__(256) unsigned char scratch[STK_NOALLOC_SCRATCH_BYTES];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[64];   // per device
+
+static int scratch_ptr(void** out)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= 64) return set_error(STK_E_INVALID, "device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (ptr == nullptr || ((uintptr_t)ptr & 255))
+            return set_error(STK_E_HIP, "hipGetSymbolAddress(scratch) returned an unusable address %p", ptr);
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+
 }  // namespace stk
 
 using namespace stk;
@@ -507,6 +543,32 @@ int stk_exact_forward(const void* X, const void* W, const float* b, float* V, in
                          workspace ? workspace_bytes : (size_t)0, p.total);
     if ((uintptr_t)workspace & 255) return set_error(STK_E_INVALID, "workspace must be 256-byte aligned");
     return run_exact(p, X, W, b, V, I, B, d, F, k, dtype, (unsigned char*)workspace, (hipStream_t)stream);
+}
+
+int stk_exact_forward_noalloc(const void* X, const void* W, const float* b, float* V, int32_t* I,
+                              int64_t B, int64_t d, int64_t F, int64_t k, int dtype, void* stream)
+{
+    clear_error();
+    int rc = validate_exact(B, d, F, k, dtype);
+    if (rc) return rc;
+    if (B == 0) return 0;
+    if ((rc = check_ptrs(X, W, b, V, I))) return rc;
+    int ncu = 0;
+    if ((rc = cu_count(&ncu))) return rc;
+    const ExactPlan p = make_exact_plan(B, d, F, k, dtype, ncu);
+    if (p.total > (size_t)STK_NOALLOC_SCRATCH_BYTES)
+        return set_error(STK_E_WORKSPACE,
+                         "this problem needs %zu bytes of workspace, more than the %zu-byte static scratch of "
+                         "stk_exact_forward_noalloc; call stk_exact_forward with a workspace",
+                         p.total, (size_t)STK_NOALLOC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    if ((rc = scratch_ptr(&ws))) return rc;
+    // no profiling events either (creating one may allocate)
+    const int prof = g_prof;
+    g_prof = 0;
+    rc = run_exact(p, X, W, b, V, I, B, d, F, k, dtype, (unsigned char*)ws, (hipStream_t)stream);
+    g_prof = prof;
+    return rc;
 }
 
 int stk_exact_forward_shard(const void* X, const void* W, const float* b, float* V, int32_t* I,

@@ -29,6 +29,7 @@ SIGNATURES = {
                                  ctypes.c_size_t, _vp]),
     "stk_exact_forward_shard": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _i64,
                                        _vp, ctypes.c_size_t, _vp]),
+    "stk_exact_forward_noalloc": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp]),
     "stk_topk_merge_workspace_bytes": (_int, [_i64, _i64, _i64, _szp]),
     "stk_topk_merge": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
     "stk_approx_workspace_bytes": (_int, [_i64, _i64, _i64, _i64, _i64, _int, _int, _szp]),

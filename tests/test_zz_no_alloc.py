@@ -1,0 +1,80 @@
+"""stk_exact_forward_noalloc: the exact encode in the library's static device
+scratch (no workspace argument, nothing allocated), called through the C ABI
+and checked against stk_exact_forward on the same inputs -- bit for bit, since
+both run the same kernels in the same order -- on two calls in a row on the
+shared scratch, the second with a smaller input, and against the float64
+oracle scores at the bf16 tolerance.  A problem larger than the scratch is
+rejected before any device work."""
+import ctypes
+
+import pytest
+import torch
+
+from parity import check_against_scores
+from streamtopk_sae import _lib, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _outputs(B, k, dev):
+    return (torch.empty((B, k), dtype=torch.float32, device=dev),
+            torch.empty((B, k), dtype=torch.int32, device=dev))
+
+
+def _with_workspace(X, W, b, k):
+    lib = _lib.load()
+    B, d = X.shape
+    F = W.shape[0]
+    nb = ctypes.c_size_t(0)
+    _lib.check(lib.stk_exact_workspace_bytes(B, d, F, k, _lib.STK_DTYPE_BF16, ctypes.byref(nb)))
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=X.device)
+    V, I = _outputs(B, k, X.device)
+    _lib.check(lib.stk_exact_forward(_p(X), _p(W), _p(b), _p(V), _p(I), B, d, F, k, _lib.STK_DTYPE_BF16,
+                                     _p(ws), nb.value, _stream()))
+    return V, I
+
+
+def _no_alloc(X, W, b, k):
+    lib = _lib.load()
+    B, d = X.shape
+    F = W.shape[0]
+    V, I = _outputs(B, k, X.device)
+    _lib.check(lib.stk_exact_forward_noalloc(_p(X), _p(W), _p(b), _p(V), _p(I), B, d, F, k,
+                                             _lib.STK_DTYPE_BF16, _stream()))
+    return V, I
+
+
+def test_noalloc_matches_workspace_entry(cuda_dev):
+    # the headline shape (27.6 MB of scratch), then a smaller problem in the
+    # same scratch: nothing of the first call may leak into the second
+    shapes = [(128, 2048, 262144, 64, 0), (40, 256, 20000, 16, 1)]
+    for B, d, F, k, seed in shapes:
+        print(f"case noalloc B={B} d={d} F={F} k={k}", flush=True)
+        X, W, b = make_inputs(B, d, F, torch.bfloat16, seed=seed, device=cuda_dev)
+        Vn, In = _no_alloc(X, W, b, k)
+        Vw, Iw = _with_workspace(X, W, b, k)
+        torch.cuda.synchronize()
+        assert torch.equal(Vn, Vw) and torch.equal(In, Iw)
+        S = (X.double() @ W.double().T + b.double()).cpu().numpy()
+        check_against_scores(Vn.cpu().numpy(), In.cpu().numpy(), S, k, 2e-3, f"noalloc B={B}")
+
+
+def test_noalloc_rejects_oversized_problem(cuda_dev):
+    """Config 4 (B=1024, d=4096, F=2^18, k=128) needs ~168 MB of workspace:
+    rejected with STK_E_WORKSPACE before anything is launched (the pointers
+    are small real tensors that the call never reads)."""
+    lib = _lib.load()
+    X = torch.zeros(16, dtype=torch.bfloat16, device=cuda_dev)
+    V, I = _outputs(1, 1, cuda_dev)
+    rc = lib.stk_exact_forward_noalloc(_p(X), _p(X), _p(V), _p(V), _p(I), 1024, 4096, 262144, 128,
+                                       _lib.STK_DTYPE_BF16, _stream())
+    assert rc == 3
+    assert "static scratch" in lib.stk_last_error().decode()
