@@ -193,36 +193,48 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     X, W, b = make_inputs(B, d, F, dtype, seed=args.seed, device=dev, heavy_tail=wl.get("heavy", False))
+    # A W smaller than ~3x the 256 MiB MALL (config 1: 96 MiB) would be served
+    # from the MALL on every step after the first: successive steps rotate over
+    # copies of W (same values) totalling at least 768 MiB, so that each step
+    # streams its W from HBM.
+    w_bytes_all = W.numel() * W.element_size()
+    n_copies = max(1, -(-768 * 2**20 // w_bytes_all))
+    W_copies = [W] + [W.clone() for _ in range(n_copies - 1)]
+    rot = [0]
+
+    def next_w():
+        w = W_copies[rot[0] % n_copies]
+        rot[0] += 1
+        return w
     torch.cuda.synchronize()
     lib = _lib.load()
 
     if wl["op"] == "exact":
         def step():
-            return topk_sae_cuda_exact(X, W, b, k)
+            return topk_sae_cuda_exact(X, next_w(), b, k)
         main_name = "main_kernel"
     elif wl["op"] == "approx":
         c = wl["c"]
 
         def step():
-            return topk_sae_cuda_approx(X, W, b, k, c)
+            return topk_sae_cuda_approx(X, next_w(), b, k, c)
         main_name = "main_kernel"
     else:
         c = wl["c"]
         cand = torch.empty((B, (F + 127) // 128, c), dtype=torch.float32, device=dev)
 
         def step():
-            return topk_sae_cuda_approx(X, W, b, k, c, candidate_buffer=cand)
+            return topk_sae_cuda_approx(X, next_w(), b, k, c, candidate_buffer=cand)
         main_name = "group_kernel"
 
     # The plain-read ceiling: a read stream over W's bytes, timed with the same
-    # in-packet events as the streaming kernel.
+    # in-packet events as the streaming kernel (rotating over the copies too).
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
-    w_bytes_all = W.numel() * W.element_size()
     stream_ptr = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
     def probe():
-        _lib.check(lib.stk_read_probe(ctypes.c_void_p(W.data_ptr()), w_bytes_all, ctypes.c_void_p(sink.data_ptr()),
-                                      stream_ptr))
+        _lib.check(lib.stk_read_probe(ctypes.c_void_p(next_w().data_ptr()), w_bytes_all,
+                                      ctypes.c_void_p(sink.data_ptr()), stream_ptr))
 
     for _ in range(20):
         probe()
@@ -333,7 +345,8 @@ def main():
         "dtype": dtn,
         "data": f"synthetic: X~N(0,1), W_enc rows N(0,1/d) then L2-normalised, b_enc~N(0,0.1^2); seed {args.seed}",
         "config": {"workload": f"{args.workload}: {wl['label']}", "op": wl["op"], "B": B, "d": d, "F": F,
-                   "k": k, **({"c": wl["c"]} if "c" in wl else {})},
+                   "k": k, **({"c": wl["c"]} if "c" in wl else {}),
+                   **({"W_copies_rotated": n_copies} if n_copies > 1 else {})},
         "roofline": roof,
         "pipeline": {"W_GBps_effective": round(w_bytes / (ms_per_step * 1e-3) / 1e9, 1),
                      "alg_bytes_per_step": alg_total,

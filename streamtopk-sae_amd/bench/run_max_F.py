@@ -4,6 +4,11 @@ columns).  A cell that fails for any reason counts as not fitting.
 
   python -m bench.run_max_F --out results/max_F.csv
   python -m bench.run_max_F --dry-run
+  python -m bench.run_max_F --configs 1 --max-pow 28   # past the reference's 2^22 cap
+
+The reference's range (2^22 at most) was sized for a 24 GB card; on a 288 GB
+MI355X every implementation reaches it at these configs, so --max-pow extends
+the search to show where each one actually stops.
 """
 import torch
 
@@ -21,16 +26,20 @@ FIELDS = ["impl", "B", "d", "k", "dtype", "max_F"]
 
 
 def fits(impl_name, B, d, F, k, dtype):
+    ok = False
     try:
         torch.cuda.empty_cache()
         X, W, b = make_inputs(B, d, F, dtype=dtype, device="cuda")
         common.IMPL_FNS[impl_name](X, W, b, k)
         torch.cuda.synchronize()
-        return True
+        ok = True
     except Exception:
-        return False
+        ok = False
     finally:
+        X = W = b = None
         torch.cuda.empty_cache()
+    print(f"# {impl_name} B={B} d={d} F={F}: {'fits' if ok else 'does not fit'}", flush=True)
+    return ok
 
 
 def max_F(impl_name, B, d, k, dtype, lo=F_MIN_POW, hi=F_MAX_POW):
@@ -47,16 +56,19 @@ def max_F(impl_name, B, d, k, dtype, lo=F_MIN_POW, hi=F_MAX_POW):
 def main(argv=None):
     parser = common.new_parser(__doc__, "results/max_F.csv")
     parser.add_argument("--impl", default=",".join(IMPLS))
+    parser.add_argument("--configs", default=None, help="indices into CONFIGS, e.g. 1 or 0,1")
+    parser.add_argument("--max-pow", type=int, default=F_MAX_POW, help="largest log2(F) searched")
     args = parser.parse_args(argv)
     rows = []
-    for cfg in (CONFIGS[:1] if args.dry_run else CONFIGS):
+    cfgs = CONFIGS if args.configs is None else [CONFIGS[int(i)] for i in common.parse_strs(args.configs)]
+    for cfg in (CONFIGS[:1] if args.dry_run else cfgs):
         B, d, k, dt = cfg["B"], cfg["d"], cfg["k"], cfg["dtype"]
         for impl_name in common.parse_strs(args.impl):
             if args.dry_run:
                 F = 2 ** F_MIN_POW
                 m = F if fits(impl_name, B, d, F, k, str_to_dtype(dt)) else None
             else:
-                m = max_F(impl_name, B, d, k, str_to_dtype(dt))
+                m = max_F(impl_name, B, d, k, str_to_dtype(dt), hi=args.max_pow)
             row = {"impl": impl_name, "B": B, "d": d, "k": k, "dtype": dt,
                    "max_F": m if m is not None else "OOM"}
             rows.append(row)
