@@ -107,7 +107,8 @@ __device__ __forceinline__ void bitonic_half(T (&v)[8], int l)
     if constexpr (STRIDE > 1) bitonic_half<STRIDE / 2>(v, l);
 }
 
-// Sorts the row's 128 keys into descending order: entry e = 8l + j.
+// Sorts the row's 128 keys into descending order: entry e = 8l + j.  With
+// SIZE < 128, sorts every aligned block of SIZE entries instead.
 template <int SIZE = 128, class T>
 __device__ __forceinline__ void bitonic_sort128(T (&v)[8], int l)
 {
@@ -116,7 +117,37 @@ __device__ __forceinline__ void bitonic_sort128(T (&v)[8], int l)
     if constexpr (SIZE >= 4) bitonic_half<SIZE / 4>(v, l);
 }
 
-template <int DT, int NB>
+// The row's top C (C = 16, 32, 64) in entries 0 .. C-1, descending, without
+// sorting all 128: every aligned block of C entries is sorted, then blocks
+// are merged pairwise keeping the larger half -- entry e of a block against
+// the mirrored entry e ^ (SIZE - 1) of its partner block, the larger kept,
+// which leaves each block a bitonic sequence holding the pair's top C, sorted
+// again by the half-cleaners of size C.  Both blocks of a pair end up with the
+// same sorted top C, so at the next level every block's mirror partner is a
+// copy of the other half's top C.  Entries C .. 127 hold copies.
+template <int C, int SIZE = 2 * C, class T>
+__device__ __forceinline__ void bitonic_topc_merge(T (&v)[8], int l)
+{
+    if constexpr (SIZE <= 128) {
+        static_assert(SIZE >= 16, "cross-lane partner blocks");
+        T o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = row_xor<SIZE / 8 - 1>(v[7 - j]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = kmax(v[j], o[j]);
+        bitonic_half<C / 2>(v, l);
+        bitonic_topc_merge<C, SIZE * 2>(v, l);
+    }
+}
+
+template <int C, class T>
+__device__ __forceinline__ void bitonic_topc(T (&v)[8], int l)
+{
+    bitonic_sort128<C, T>(v, l);
+    if constexpr (C < 128) bitonic_topc_merge<C>(v, l);
+}
+
+template <int DT, int NB, int C>
 __global__ __launch_bounds__(kMainThreads, 1) void group_kernel(GroupArgs a)
 {
     using TS = TileStream<DT, NB, kMainWaves>;
@@ -130,7 +161,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void group_kernel(GroupArgs a)
     const int l = lane & 15, sq = lane >> 4;
     const int64_t b0 = (int64_t)blockIdx.y * (32 * NB);
     const int64_t B = a.B, F = a.F, G = a.num_groups;
-    const int c = a.c;
+    constexpr int c = C;   // a.c
     const int64_t num_tiles = (G + 1) / 2;
 
     TS ts;
@@ -189,14 +220,32 @@ __global__ __launch_bounds__(kMainThreads, 1) void group_kernel(GroupArgs a)
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
                     v[j] = ((j < 4 ? w0[j] : w1[j - 4]) & ~0x7Fu) | (uint32_t)(127 - (8 * l + j));
-                bitonic_sort128(v, l);
+                // c < 128: only the top c are selected and ordered (entries c ..
+                // 127 end up holding copies); c = 128: the full sort
+                bitonic_topc<C>(v, l);
                 const uint32_t nx = __shfl_down(v[0], 1, 16);   // entry 8l + 8
                 bool tie = false;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const uint32_t y = j < 7 ? v[j + 1] : nx;
-                    const bool last = j == 7 && l == 15;
-                    tie |= !last && 8 * l + j < c && (y >> 7) != 0 && (v[j] >> 7) == (y >> 7);
+                    tie |= 8 * l + j < c - 1 && (y >> 7) != 0 && (v[j] >> 7) == (y >> 7);
+                }
+                if constexpr (C < 128) {
+                    // the (c+1)-th is not at hand: a real entry outside the top c
+                    // whose truncated word equals the c-th's shows as more than c
+                    // real entries at or above that word
+                    const uint32_t tc = __shfl(v[7], c / 8 - 1, 16) >> 7;   // entry c - 1
+                    int above = 0;
+                    // the words again from LDS, rather than held through the network
+                    const u32x4 r0 = *(const u32x4*)(src + 8 * l), r1 = *(const u32x4*)(src + 8 * l + 4);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const uint32_t ov = j < 4 ? r0[j] : r1[j - 4];
+                        above += (ov != 0u && (ov >> 7) >= tc) ? 1 : 0;
+                    }
+#pragma unroll
+                    for (int m = 1; m < 16; m <<= 1) above += __shfl_xor(above, m, 16);
+                    tie |= tc != 0u && above != c;
                 }
                 float val[8];
                 uint32_t idx[8];
@@ -212,9 +261,10 @@ __global__ __launch_bounds__(kMainThreads, 1) void group_kernel(GroupArgs a)
                 } else {
                     // full keys for this wave's four segments
                     uint64_t u[8];
+                    const u32x4 r0 = *(const u32x4*)(src + 8 * l), r1 = *(const u32x4*)(src + 8 * l + 4);
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
-                        const uint32_t ov = j < 4 ? w0[j] : w1[j - 4];
+                        const uint32_t ov = j < 4 ? r0[j] : r1[j - 4];
                         u[j] = ov ? (((uint64_t)ov << 32) | (0xFFFFFFFFu - (fg + 8 * l + j))) : 0ull;
                     }
                     bitonic_sort128(u, l);
@@ -322,15 +372,27 @@ __global__ __launch_bounds__(kThreads) void cand_kernel(CandArgs a)
     }
 }
 
-template <int DT, int NB>
-static hipError_t launch_group_t(const GroupArgs& a, dim3 grid, hipStream_t st)
+template <int DT, int NB, int C>
+static hipError_t launch_group_c(const GroupArgs& a, dim3 grid, hipStream_t st)
 {
     const size_t lds = group_lds_bytes(NB);
-    auto kern = group_kernel<DT, NB>;
+    auto kern = group_kernel<DT, NB, C>;
     hipError_t e = ensure_lds((const void*)kern, lds);
     if (e != hipSuccess) return e;
     launch(kern, grid, dim3(kMainThreads), lds, st, a);
     return hipGetLastError();
+}
+
+template <int DT, int NB>
+static hipError_t launch_group_t(const GroupArgs& a, dim3 grid, hipStream_t st)
+{
+    switch (a.c) {
+    case 16: return launch_group_c<DT, NB, 16>(a, grid, st);
+    case 32: return launch_group_c<DT, NB, 32>(a, grid, st);
+    case 64: return launch_group_c<DT, NB, 64>(a, grid, st);
+    case 128: return launch_group_c<DT, NB, 128>(a, grid, st);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_group(int dt, int NB, const GroupArgs& a, dim3 grid, hipStream_t st)
