@@ -4,6 +4,7 @@
 // every temporary lives in the caller's workspace.
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -264,7 +265,7 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
     p.off_thr = off;
     off = align256(off + (size_t)B * 8);
     p.off_lcnt = off;
-    off = align256(off + (size_t)B * 4 * kCntStride);
+    off = align256(off + (size_t)B * 4 * kCntStride + 4 * kCntStride);   // + the error word's line
     p.off_seg = off;
     off = align256(off + (size_t)B * p.nwg * 4);
     p.off_list = off;
@@ -326,6 +327,10 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     uint64_t* list_keys = (uint64_t*)(ws + p.off_list);
     int32_t* list_cnt = (int32_t*)(ws + p.off_lcnt);
     int32_t* seg_cnt = (int32_t*)(ws + p.off_seg);
+    uint32_t* err = (uint32_t*)(list_cnt + B * kCntStride);
+    // STK_TEST_MAX_ROUNDS: the test hook that lowers the retry bounds
+    int max_rounds = -1;
+    if (const char* env = std::getenv("STK_TEST_MAX_ROUNDS")) max_rounds = std::atoi(env);
     // the sample's partial sums: in each row's segment area, split after split
     float* P = p.sample ? (float*)(list_keys + p.head_span) : nullptr;
     const int64_t p_row = 2 * p.list_cap, p_split = p.nsamp;
@@ -369,6 +374,7 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     ta.bias = b;
     ta.samp_log2 = p.samp_log2; ta.nsamp = p.nsamp; ta.k = (int)k;
     ta.thr = thr; ta.list_keys = list_keys; ta.list_cnt = list_cnt; ta.list_cap = p.list_cap;
+    ta.err = err;
     int pt = prof_begin("thr_kernel", st);
     e = launch_thr(ta, B, st);
     prof_end(pt, st);
@@ -387,6 +393,8 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         ml.samp_blocks = p.nsamp / kSampleBlock;
         ml.list_keys = list_keys; ml.list_cap = p.list_cap; ml.head_span = p.head_span;
         ml.seg_cnt = seg_cnt;
+        ml.max_rounds = max_rounds >= 0 ? max_rounds : kMainLMaxRounds;
+        ml.err = err;
         int pm = prof_begin("main_kernel", st);
         e = launch_mainl(dt, ml, (int)(p.nbc * p.nwg), st);
         prof_end(pm, st);
@@ -406,6 +414,8 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         ma.list_keys = list_keys; ma.list_cap = p.list_cap; ma.head_span = p.head_span;
         ma.seg_cnt = seg_cnt;
         ma.lq = p.lq;
+        ma.max_rounds = max_rounds >= 0 ? max_rounds : kMainMaxRounds;
+        ma.err = err;
         int pm = prof_begin("main_kernel", st);
         e = launch_main(dt, p.NB, ma, dim3((unsigned)p.nwg, (unsigned)p.nbc), st);
         prof_end(pm, st);
@@ -421,6 +431,7 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     }
     mg.k = (int)k;
     mg.f_offset = (int32_t)f_offset;
+    mg.err = err;
     mg.V = V; mg.I = I;
     const int pg = prof_begin("merge_kernel", st);
     e = launch_merge(mg, B, st);
@@ -655,6 +666,7 @@ int stk_topk_merge(const float* Vp, const int32_t* Ip, int64_t nparts, int64_t B
     mg.spec = nparts * k > 4096 ? 1 : 0;
     mg.k = (int)k;
     mg.f_offset = 0;
+    mg.err = nullptr;
     mg.V = V; mg.I = I;
     const int pg = prof_begin("merge_kernel", st);
     e = launch_merge(mg, B, st);

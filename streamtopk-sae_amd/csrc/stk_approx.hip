@@ -277,7 +277,14 @@ __global__ __launch_bounds__(kMainThreads, 1) void group_kernel(GroupArgs a)
                 const int64_t row = b0 + 32 * n + rl;
                 const int64_t grp = 2 * tile + g;
                 if (row < B && grp < G && 8 * l < c) {
-                    const int64_t o = (row * G + grp) * c + 8 * l;
+                    // the block's uniform part, then this lane's, recomputed at
+                    // every store (the empty asm hides rl's invariance: hoisted,
+                    // the 64-bit lane offsets of every block would be held in
+                    // registers through the tile loop, and spilled)
+                    const int64_t ob = ((b0 + 32 * n) * G + 2 * tile) * c;
+                    int rlv = rl;
+                    asm volatile("" : "+v"(rlv));
+                    const int64_t o = ob + ((int64_t)rlv * G + g) * c + 8 * l;
                     *(f32x4*)(a.cand_vals + o) = f32x4{val[0], val[1], val[2], val[3]};
                     *(f32x4*)(a.cand_vals + o + 4) = f32x4{val[4], val[5], val[6], val[7]};
                     *(u32x4*)(a.cand_idxs + o) = u32x4{idx[0], idx[1], idx[2], idx[3]};

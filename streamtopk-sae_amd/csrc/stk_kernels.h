@@ -76,10 +76,23 @@ struct MainArgs {
                                  //   per workgroup (gridDim.x of them)
     int32_t* seg_cnt;            // [B][gridDim.x] keys each workgroup left in its segment
     int lq;                      // LDS queue keys per row (even, <= 64; cap >= k + lq)
+    int max_rounds;              // bound of the epilogue's spill-and-retry loop
+    uint32_t* err;               // set non-zero if that bound is ever reached
 };
 
 // Row r's head count is list_cnt[r * kCntStride]: one 128-byte line per row.
 constexpr int kCntStride = 32;
+
+// The spill-and-retry loops of the streaming kernels end after a bounded
+// number of rounds.  The bounds are never reached (main_kernel places at least
+// lq >= 8 of a row's <= 256 pending scores per round, mainl_kernel at least
+// cap - k >= 64), so they only guard against a broken invariant: reaching one
+// sets the workspace's error word, and the merge then marks every row of its
+// output (indices -1, values NaN) instead of returning a silently wrong
+// result.  STK_TEST_MAX_ROUNDS=n in the environment allows n spill rounds
+// instead (a test hook that forces that path from the host; 0: none).
+constexpr int kMainMaxRounds = 4096;
+constexpr int kMainLMaxRounds = 1 << 20;
 
 constexpr int kSampleWaves = 8;      // wavefronts per sample_kernel workgroup
 constexpr int kSampleThreads = 64 * kSampleWaves;
@@ -106,6 +119,7 @@ struct ThrArgs {
     uint64_t* list_keys;         // [B][list_cap]: receives the sampled keys >= thr
     int32_t* list_cnt;           // [B * kCntStride] set to the number of those keys
     int64_t list_cap;
+    uint32_t* err;               // the call's error word, cleared by row 0's workgroup
 };
 
 // Large-batch streaming kernel: 256 rows x 256 latents per tile, queues in
@@ -127,6 +141,8 @@ struct MainLArgs {
     uint64_t* list_keys;         // [B][list_cap]: head_span head slots, then nr segments of cap
     int64_t list_cap, head_span;
     int32_t* seg_cnt;            // [B][nr] keys in each segment
+    int max_rounds;              // bound of the overflow loop (see kMainLMaxRounds)
+    uint32_t* err;
     // sample mode (mainl_sample_kernel): 256-latent tiles of the sampled
     // latents, d split in ksplit ranges; raw partial scores to P
     int ksplit, nsamp;
@@ -153,6 +169,7 @@ struct MergeArgs {
                                  //   3, 4: merge_seg_kernel (head <= 256 keys, one
                                  //   segment per thread; 30 or 62 keys per pass)
     int32_t f_offset;            // added to every emitted index (a shard's first latent)
+    const uint32_t* err;         // non-zero: mark the output rows (-1, NaN); may be null
     float* V;
     int32_t* I;
 };

@@ -186,7 +186,7 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
         // one a slot per thread that absorbs the writes of overflowing survivors.
         float* sc = (float*)(smem + TS::kWBuf) + wave * 16 * 64;
         uint64_t* dump = (uint64_t*)(smem + 2 * TS::kWBuf + TS::kXBuf) + tid;
-        for (int it = 0; it < 4096; ++it) {
+        for (int it = 0;; ++it) {
             bool overflow = false;
             // reserve the slots of every row block first, then wait once
             int base[NB];
@@ -213,6 +213,12 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
                 overflow |= keep != 0;
             }
             if (!__syncthreads_or(overflow)) break;
+            if (it >= a.max_rounds) {
+                // unreachable by the bound's argument (kMainMaxRounds): the
+                // pending scores are lost, so the call's result is marked
+                if (tid == 0) atomicOr(a.err, 1u);
+                break;
+            }
             __syncthreads();   // the LDS queues are complete
             spill_rows<R>(cnt, gcnt, thr, lqk, seg, a.list_cap, cscr + wave * cap, lq, cap, k, wave, lane, false);
             __syncthreads();
@@ -379,6 +385,7 @@ __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
     __shared__ SelShared S;
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
+    if (row == 0 && tid == 0) *a.err = 0u;   // the first kernel that runs after it is read
     if (a.P == nullptr) {
         if (tid == 0) { a.thr[row] = 0; a.list_cnt[row * kCntStride] = 0; }
         return;
@@ -513,6 +520,19 @@ __device__ __forceinline__ void merge_pass(SelShared& S, const uint64_t (&v)[N],
 // at once, unconditionally (clamped into the row's list, masked afterwards),
 // together with the row's count; every other slot is loaded only if it holds
 // a candidate.
+// Whether the call's error word is set (a streaming kernel lost candidates);
+// if so, row `row` of the output is marked: indices -1, values NaN.  The word
+// is the same for every thread, so the whole workgroup returns together.
+__device__ __forceinline__ bool merge_marked(const MergeArgs& a, int64_t row, int tid)
+{
+    if (a.err == nullptr || *a.err == 0u) return false;
+    for (int r = tid; r < a.k; r += kThreads) {
+        a.V[row * a.k + r] = __builtin_nanf("");
+        a.I[row * a.k + r] = -1;
+    }
+    return true;
+}
+
 template <int kPer, int kSpec>
 __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
 {
@@ -521,6 +541,7 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
     __shared__ int spre[kMergeMaxSeg];   // inclusive prefix sums of scnt
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
+    if (merge_marked(a, row, tid)) return;
     const int k = a.k;
     const int nseg = a.nseg;
     const int64_t hc = a.list_cnt[row * kCntStride];
@@ -622,6 +643,7 @@ __global__ __launch_bounds__(kThreads) void merge_seg_kernel(MergeArgs a)
     __shared__ SelShared S;
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
+    if (merge_marked(a, row, tid)) return;
     const int k = a.k;
     const int nseg = a.nseg;
     const int64_t hs = a.head_span;   // <= kThreads (host)

@@ -529,7 +529,13 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                     uint64_t pend = ovf[n];
                     if (!__syncthreads_or(pend != 0)) return;
                     stage_block(nc, 0.f);   // this block's scores back into the staging area
-                    for (int it = 0; it < 1 << 20; ++it) {
+                    for (int it = 0;; ++it) {
+                        if (it >= a.max_rounds) {
+                            // unreachable by the bound's argument (kMainLMaxRounds):
+                            // the pending scores are lost, so the result is marked
+                            if (tid == 0) atomicOr(a.err, 1u);
+                            break;
+                        }
                         __threadfence_block();   // this thread's segment stores are complete
                         __syncthreads();
                         compact_full_rows<kLargeRows / kLWaves>(cnt, thr, cscr + wave * cap,

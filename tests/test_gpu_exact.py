@@ -300,3 +300,27 @@ def test_exact_config4_shape(cuda_dev, heavy):
     print(f"case config4 heavy={heavy}", flush=True)
     X, W, b = make_inputs(1024, 4096, 262144, torch.bfloat16, seed=0, device=cuda_dev, heavy_tail=heavy)
     _run_check(X, W, b, 128, "bf16", scores="torch64", name=f"config4/heavy={heavy}")
+
+
+@pytest.mark.parametrize("B,F,k", [(64, 20480, 64), (512, 8000, 128)])
+def test_retry_bound_marks_output(cuda_dev, monkeypatch, B, F, k):
+    """The streaming kernels' spill-and-retry loops are bounded.  With the
+    bound forced down from the host (STK_TEST_MAX_ROUNDS, which the library
+    reads at each call), scores that rise along F overflow every tile and
+    reach it: the call then marks its output (indices -1, values NaN) rather
+    than returning a result with candidates missing.  With the default bounds
+    the same inputs give the exact answer.  B=64 runs main_kernel, B=512
+    mainl_kernel."""
+    print(f"case retry bound B={B} F={F} k={k}", flush=True)
+    d = 64
+    X = torch.ones(B, d, dtype=torch.float32, device=cuda_dev)
+    W = torch.zeros(F, d, dtype=torch.float32, device=cuda_dev)
+    b = torch.arange(F, dtype=torch.float32, device=cuda_dev) * 1e-3
+    monkeypatch.setenv("STK_TEST_MAX_ROUNDS", "0")
+    V, I = topk_sae_cuda_exact(X, W, b, k)
+    assert bool((I == -1).all()) and bool(torch.isnan(V).all())
+    monkeypatch.delenv("STK_TEST_MAX_ROUNDS")
+    V, I = topk_sae_cuda_exact(X, W, b, k)
+    want = np.arange(F - 1, F - 1 - k, -1)
+    assert all(np.array_equal(r, want) for r in I.cpu().numpy())
+    assert np.array_equal(V[0].cpu().numpy(), b.cpu().numpy()[want])

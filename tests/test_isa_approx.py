@@ -3,9 +3,10 @@ gfx950 assembly of csrc/stk_approx.hip, compiled here with the build's flags.
 
 group_kernel keeps a whole tile of accumulators and eight sort keys per lane
 in registers (8 waves per workgroup, so at most 256 VGPRs per lane): a spill
-or an indexed key array would put the sort network in scratch memory.  The
-lane exchanges of the sort must stay DPP moves (fused into the min / max when
-the compiler can) apart from the one stride that goes through ds_bpermute.
+or an indexed key array would put the sort network in scratch memory.  Every
+instantiation (dtype x row blocks x c) is checked.  The lane exchanges of the
+full sort (c = 128) must stay DPP moves (fused into the min / max when the
+compiler can) apart from the one stride that goes through ds_bpermute.
 """
 import os
 import re
@@ -40,7 +41,11 @@ def _kernel(asm, name):
     return body, asm[start:end if end > 0 else len(asm)]
 
 
-GROUP = [f"_ZN3stk12group_kernelILi{dt}ELi{nb}EEEvNS_9GroupArgsE" for dt in (0, 1, 2) for nb in (1, 2, 4)]
+def _group(dt, nb, c):
+    return f"_ZN3stk12group_kernelILi{dt}ELi{nb}ELi{c}EEEvNS_9GroupArgsE"
+
+
+GROUP = [_group(dt, nb, c) for dt in (0, 1, 2) for nb in (1, 2, 4) for c in (16, 32, 64, 128)]
 
 
 @pytest.mark.parametrize("name", GROUP + ["_ZN3stk11cand_kernelENS_8CandArgsE"])
@@ -53,7 +58,7 @@ def test_no_scratch_no_spill(asm, name):
 
 @pytest.mark.parametrize("nb", [1, 2, 4])
 def test_sort_exchanges(asm, nb):
-    body, meta = _kernel(asm, f"_ZN3stk12group_kernelILi2ELi{nb}EEEvNS_9GroupArgsE")
+    body, meta = _kernel(asm, _group(2, nb, 128))
     assert int(re.search(r"\.vgpr_count:\s+(\d+)", meta).group(1)) <= 256
     dpp = len(re.findall(r"\bv_\w+_dpp\b", body))
     # per sort: 9 of the 10 exchange stages are DPP (the flips of 16 .. 128
