@@ -211,7 +211,7 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
     // ranges to fill the device
     p.ksplit = 1;
     p.snb = 1;
-    const int64_t nds = d / (dtype == STK_DTYPE_F32 ? 32 : 64);
+    const int64_t nds = cdiv(d, dtype == STK_DTYPE_F32 ? 32 : 64);   // d-steps, the last maybe partial
     if (p.large && p.sample) {
         const int64_t wgs = p.nbc * (p.nsamp / kTileLatents);
         int64_t ks = cdiv(ncu, wgs);
@@ -286,8 +286,10 @@ static int check_shape_common(int64_t B, int64_t d, int64_t F, int dtype)
     if (B < 0 || d < 1 || F < 1) return set_error(STK_E_INVALID, "invalid shape: B=%lld d=%lld F=%lld",
                                                   (long long)B, (long long)d, (long long)F);
     if (F > 0x7FFFFFFELL) return set_error(STK_E_INVALID, "F=%lld exceeds the int32 index range", (long long)F);
-    // one d-step is 128 bytes of a row: 64 fp16/bf16 or 32 fp32 elements
-    const int64_t q = (dtype == STK_DTYPE_F32) ? 32 : 64;
+    // rows are read in 16-byte chunks (8 fp16/bf16 or 4 fp32 elements); a d
+    // that is not a whole number of 128-byte d-steps ends in a partial step
+    // whose chunks past d read as zeros
+    const int64_t q = (dtype == STK_DTYPE_F32) ? 4 : 8;
     if (d % q)
         return set_error(STK_E_INVALID,
                          "d=%lld must be a multiple of %lld for %s inputs (pad X and W_enc with zero columns)",

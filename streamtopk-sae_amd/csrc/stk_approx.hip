@@ -174,7 +174,8 @@ __global__ __launch_bounds__(kMainThreads, 1) void group_kernel(GroupArgs a)
         const int64_t t1 = ts.tile_begin + a.tiles_per_wg;
         ts.ntiles = (int)((t1 < num_tiles ? t1 : num_tiles) - ts.tile_begin);
     }
-    ts.nds = (int)(a.d / Dt<DT>::DS);
+    ts.nds = (int)((a.d + Dt<DT>::DS - 1) / Dt<DT>::DS);
+    ts.tail = (int)(a.d % Dt<DT>::DS);
     ts.nds2 = (ts.nds + 1) / 2 * 2;
     ts.tid = tid;
     ts.lane = lane;

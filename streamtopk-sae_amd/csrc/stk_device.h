@@ -232,10 +232,13 @@ struct TileStream {
     static_assert(kXTotal % kThr == 0 || kXChunks == 1, "X chunk split");
     static_assert(kTileF * 8 % kThr == 0, "W chunk split");
 
+    static constexpr int kQE = 16 / ES;                            // elements per 16-byte chunk
+
     const float* bias;
     int64_t F;
     int64_t tile_begin;
     int ntiles, nds, nds2;
+    int tail;                    // elements of d in the last d-step when it is partial, else 0
     int tid, lane, wave, h, jl;
     const unsigned char* W;
     int64_t w_row_bytes;
@@ -275,10 +278,29 @@ struct TileStream {
     {
         const int s = (lt >= ntiles || ls >= nds) ? nds - 1 : ls;
         const int64_t so = (int64_t)s * kStepBytes;
+        if (tail != 0 && s == nds - 1) {
+            // partial last step: a chunk past d reads the step's first chunk
+            // (in bounds: the step starts below d) and is zeroed
 #pragma unroll
-        for (int p = 0; p < kXChunks; ++p) xr[p] = *(const u32x4*)(lx[p] + so);
+            for (int p = 0; p < kXChunks; ++p) {
+                const int c8 = (tid + kThr * p) & 7;
+                const bool ok = c8 * kQE < tail;
+                const u32x4 v = *(const u32x4*)(lx[p] + so - (ok ? 0 : c8 * 16));
+                xr[p] = ok ? v : u32x4{0u, 0u, 0u, 0u};
+            }
 #pragma unroll
-        for (int p = 0; p < kWChunks; ++p) wr[p] = __builtin_nontemporal_load((const u32x4*)(lw[p] + so));
+            for (int p = 0; p < kWChunks; ++p) {
+                const int c8 = (tid + kThr * p) & 7;
+                const bool ok = c8 * kQE < tail;
+                const u32x4 v = __builtin_nontemporal_load((const u32x4*)(lw[p] + so - (ok ? 0 : c8 * 16)));
+                wr[p] = ok ? v : u32x4{0u, 0u, 0u, 0u};
+            }
+        } else {
+#pragma unroll
+            for (int p = 0; p < kXChunks; ++p) xr[p] = *(const u32x4*)(lx[p] + so);
+#pragma unroll
+            for (int p = 0; p < kWChunks; ++p) wr[p] = __builtin_nontemporal_load((const u32x4*)(lw[p] + so));
+        }
         if (lt < ntiles && ++ls == nds2) {
             ls = 0;
             ++lt;

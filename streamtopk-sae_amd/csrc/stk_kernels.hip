@@ -135,7 +135,8 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
         const int64_t t1 = ts.tile_begin + a.tiles_per_wg;
         ts.ntiles = (int)((t1 < a.num_tiles ? t1 : a.num_tiles) - ts.tile_begin);
     }
-    ts.nds = (int)(a.d / Dt<DT>::DS);
+    ts.nds = (int)((a.d + Dt<DT>::DS - 1) / Dt<DT>::DS);
+    ts.tail = (int)(a.d % Dt<DT>::DS);
     ts.nds2 = (ts.nds + 1) / 2 * 2;
     ts.tid = tid;
     ts.lane = lane;
@@ -283,7 +284,8 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a)
     const int64_t ib = (int64_t)lb * kSampleLat;
     const int64_t b0 = (int64_t)blockIdx.y * BT;
     const int64_t d = a.d;
-    const int64_t nds = d / DS;   // d is a whole number of steps (checked on the host)
+    constexpr int QE = 16 / ES;   // elements per 16-byte chunk
+    const int64_t nds = (d + DS - 1) / DS;   // the last step may be partial: its chunks past d read as zeros
     const int64_t sb = sp * nds / a.nsplit;
     const int ns = (int)((sp + 1) * nds / a.nsplit - sb);   // 1 .. kSampleSteps (host)
 
@@ -304,18 +306,25 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a)
             const int c = tid + kSampleThreads * p;
             const int c16 = c & 7, row = (c >> 3) % BT, st = (c >> 3) / BT;
             const int64_t j = b0 + row;
-            okm |= (j < a.B && st < ns) ? (1u << p) : 0u;
-            const int64_t jc = j < a.B ? j : a.B - 1;
             const int stc = st < ns ? st : ns - 1;
-            xr[p] = *(const u32x4*)((const unsigned char*)a.X + (jc * d + (sb + stc) * DS) * ES + c16 * 16);
+            const bool in_d = (sb + stc) * DS + c16 * QE < d;   // a chunk past d reads the step's first
+            okm |= (j < a.B && st < ns && in_d) ? (1u << p) : 0u;
+            const int64_t jc = j < a.B ? j : a.B - 1;
+            xr[p] = *(const u32x4*)((const unsigned char*)a.X + (jc * d + (sb + stc) * DS) * ES +
+                                    (in_d ? c16 * 16 : 0));
         }
         __builtin_amdgcn_sched_barrier(0);
-        // W of steps sl and sl + 4 (a step past the range reloads step 0; its X is zero)
+        // W of steps sl and sl + 4 (a step past the range reloads step 0; its X
+        // is zero); chunks past d read the step's first chunk and are zeroed
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             const int st = sl + 4 * t < ns ? sl + 4 * t : 0;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) w[t][q] = *(const u32x4*)(wp + st * kStepBytes + q * 16);
+            for (int q = 0; q < 4; ++q) {
+                const bool in_d = (sb + st) * DS + h * (DS / 2) + q * QE < d;
+                const u32x4 v = *(const u32x4*)(wp + st * kStepBytes + (in_d ? q * 16 : -h * 64));
+                w[t][q] = in_d ? v : u32x4{0u, 0u, 0u, 0u};
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll

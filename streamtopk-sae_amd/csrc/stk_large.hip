@@ -102,6 +102,7 @@ struct BigStream {
     int64_t B, b0, F;
     int64_t tile_begin;
     int ntiles, nds, nds2;
+    int tail;                    // elements of d in the last d-step when it is partial, else 0
     int s_lo, s_hi;              // d-steps [s_lo, s_hi) of every tile
     int samp_log2;               // SAMPLE: tile t covers sampled latents t*256 ..
     int tid, lane, wave, h, jl;
@@ -147,6 +148,16 @@ struct BigStream {
         }
     }
 
+    // The partial last d-step (tail != 0): a lane whose source chunk of load i
+    // lies past d takes an offset beyond every resource's size, so the load
+    // returns zeros.
+    __device__ __forceinline__ int tail_off(int off, int i) const
+    {
+        const int r = 8 * i + (lane >> 3);
+        const int chunk = (lane & 7) ^ xswz(r);
+        return chunk * (16 / Dt<DT>::esize) < tail ? off : 0x40000000;
+    }
+
     // W of step ws (zeros past s_hi) straight into the W stage, whole 128-byte
     // lines: this wave's 64-row run.
     __device__ __forceinline__ void issue_w(unsigned char* wst)
@@ -155,8 +166,14 @@ struct BigStream {
         const bool live = w < s_hi;
         const __amdgpu_buffer_rsrc_t r = live ? wres : zres;
         const int so = live ? w * kStepBytes : 0;
+        if (tail != 0 && w == nds - 1) {
 #pragma unroll
-        for (int i = 0; i < kLWChunks; ++i) lds_load16(r, wst + (wave * 64 + 8 * i) * kStepBytes, wvoff[i], so);
+            for (int i = 0; i < kLWChunks; ++i)
+                lds_load16(r, wst + (wave * 64 + 8 * i) * kStepBytes, tail_off(wvoff[i], i), so);
+        } else {
+#pragma unroll
+            for (int i = 0; i < kLWChunks; ++i) lds_load16(r, wst + (wave * 64 + 8 * i) * kStepBytes, wvoff[i], so);
+        }
         ++ws;
     }
 
@@ -167,8 +184,14 @@ struct BigStream {
         const bool live = x < s_hi;
         const __amdgpu_buffer_rsrc_t r = live ? xres : zres;
         const int so = live ? x * kStepBytes : 0;
+        if (tail != 0 && x == nds - 1) {
 #pragma unroll
-        for (int i = 0; i < kLXChunks; ++i) lds_load16(r, xst + (wave * 64 + 8 * i) * kStepBytes, xvoff[i], so);
+            for (int i = 0; i < kLXChunks; ++i)
+                lds_load16(r, xst + (wave * 64 + 8 * i) * kStepBytes, tail_off(xvoff[i], i), so);
+        } else {
+#pragma unroll
+            for (int i = 0; i < kLXChunks; ++i) lds_load16(r, xst + (wave * 64 + 8 * i) * kStepBytes, xvoff[i], so);
+        }
         ++xs;
     }
 
@@ -324,7 +347,8 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
     bs.B = B;
     bs.b0 = b0;
     bs.F = F;
-    bs.nds = (int)(a.d / Dt<DT>::DS);
+    bs.nds = (int)((a.d + Dt<DT>::DS - 1) / Dt<DT>::DS);
+    bs.tail = (int)(a.d % Dt<DT>::DS);
     bs.samp_log2 = a.samp_log2;
     if (SAMPLE) {
         bs.tile_begin = rg;

@@ -127,11 +127,13 @@ def topk_sae_cpu(X, W_enc, b_enc, k):
 
 
 def _device_inputs(X, W_enc, b_enc):
-    """Native-side checks, then the zero-padding of d to whole 128-byte steps
-    (32 fp32 or 64 fp16/bf16 elements) and 16-byte alignment."""
+    """Native-side checks, then 16-byte alignment.  The kernels read rows in
+    16-byte chunks and mask a partial last chunk-step themselves, so only a d
+    that leaves rows misaligned (not a multiple of 4 fp32 or 8 fp16/bf16
+    elements) is zero-padded, which copies W_enc."""
     _contiguity_checks(X, W_enc, b_enc)
     _device_checks(X, W_enc, b_enc)
-    multiple = 32 if X.dtype == torch.float32 else 64
+    multiple = 4 if X.dtype == torch.float32 else 8
     X, W_enc = _pad_d(X, W_enc, multiple)
     return _aligned(X), _aligned(W_enc), b_enc
 

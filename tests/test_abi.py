@@ -44,8 +44,8 @@ def _exact(B=4, d=64, F=256, k=8, dtype=2):
     (dict(k=512, F=256), "k out of range"),
     (dict(d=8192), "d exceeds D_MAX=4096"),
     (dict(dtype=7), "X dtype must be fp32, fp16, or bf16"),
-    (dict(d=100), "d=100 must be a multiple of 64"),
-    (dict(d=48, dtype=0), "d=48 must be a multiple of 32"),
+    (dict(d=100), "d=100 must be a multiple of 8"),
+    (dict(d=30, dtype=0), "d=30 must be a multiple of 4"),
 ])
 def test_exact_argument_errors(kw, msg):
     rc = _exact(**kw)

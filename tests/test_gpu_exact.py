@@ -88,11 +88,59 @@ def test_exact_k128_many_rows(cuda_dev):
 
 
 def test_exact_ragged_d(cuda_dev):
-    """d not a multiple of 8: the op pads X and W_enc with zero columns."""
+    """d not a multiple of 8 (fp16/bf16) or 4 (fp32): the op pads X and W_enc
+    with zero columns."""
     X, W, b = make_inputs(8, 100, 600, torch.bfloat16, seed=7, device=cuda_dev)
     _run_check(X, W, b, 16, "bf16", name="d=100")
     X, W, b = make_inputs(8, 30, 600, torch.float32, seed=7, device=cuda_dev)
     _run_check(X, W, b, 8, "fp32", name="d=30 fp32")
+
+
+# d a multiple of 16 bytes but not of one 128-byte d-step: the kernels mask
+# the partial last step themselves (no copy of W_enc).  Every streaming kernel
+# and the sample passes (F >= 16384), with row blocks past B.
+RAGGED_D = [
+    dict(B=40, d=200, F=20000, k=32, dtype_name="bf16"),      # main_kernel + sample_kernel
+    dict(B=7, d=8, F=3000, k=8, dtype_name="fp16"),           # one partial step only
+    dict(B=100, d=1000, F=17000, k=64, dtype_name="fp32"),    # fp32: 32-element steps, 8 valid in the last
+    dict(B=600, d=200, F=20000, k=64, dtype_name="bf16"),     # mainl_kernel + its sample mode
+    dict(B=520, d=36, F=3000, k=16, dtype_name="fp32"),       # mainl_kernel, one partial step per tile row
+]
+
+
+@pytest.mark.parametrize("shape", RAGGED_D, ids=lambda s: f"B{s['B']}-d{s['d']}-{s['dtype_name']}")
+def test_exact_ragged_d_in_kernel(cuda_dev, shape):
+    c = shape
+    print(f"case ragged d in kernel {c}", flush=True)
+    X, W, b = make_inputs(c["B"], c["d"], c["F"], DT[c["dtype_name"]], seed=8, device=cuda_dev)
+    nb = ctypes_workspace_bytes(c)
+    assert nb > 0   # accepted by the C ABI as is (no padding in the op)
+    _run_check(X, W, b, c["k"], c["dtype_name"], scores="torch64", name=f"ragged d {c}")
+
+
+def ctypes_workspace_bytes(c):
+    import ctypes
+    from streamtopk_sae import _lib
+    dt = {"fp32": _lib.STK_DTYPE_F32, "fp16": _lib.STK_DTYPE_F16, "bf16": _lib.STK_DTYPE_BF16}[c["dtype_name"]]
+    nb = ctypes.c_size_t(0)
+    _lib.check(_lib.load().stk_exact_workspace_bytes(c["B"], c["d"], c["F"], c["k"], dt, ctypes.byref(nb)))
+    return nb.value
+
+
+@pytest.mark.parametrize("c", [16, 128])
+def test_approx_ragged_d_in_kernel(cuda_dev, c):
+    """The candidate-buffer kernel with a partial last d-step (d = 200 bf16)."""
+    print(f"case approx ragged d c={c}", flush=True)
+    B, d, F, k = 40, 200, 3000, 16
+    X, W, b = make_inputs(B, d, F, torch.bfloat16, seed=9, device=cuda_dev)
+    cb = torch.empty((B, (F + 127) // 128, c), dtype=torch.float32, device=cuda_dev)
+    from streamtopk_sae import topk_sae_cuda_approx
+    V, I = topk_sae_cuda_approx(X, W, b, k, c, candidate_buffer=cb)
+    _, _, cvo, cio = oracle.approx(_np(X), _np(W), _np(b), k, c, with_candidates=True)
+    err = np.abs(cb.cpu().numpy() - cvo) / np.maximum(np.abs(cvo), 1.0)
+    assert err.max() <= 2e-3
+    S = _oracle_scores(X, W, b)
+    check_against_scores(V.cpu().numpy(), I.cpu().numpy(), S, k, 2e-3, "approx ragged d")
 
 
 def test_edge_k_equals_F(cuda_dev):
