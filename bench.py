@@ -249,6 +249,12 @@ def main():
     probe_us = 1e3 * probe_rec.value / probe_n.value
     _lib.check(lib.stk_profile_enable(0))
 
+    # Memory: everything the op allocates from its first call on, the workspace
+    # it keeps per stream included, over the resident inputs.
+    torch.cuda.synchronize()
+    base_mem = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+
     # Device settle: untimed calls of the step for --settle seconds before the
     # W warmup steps.  Short runs that start from another load (or from idle)
     # come out 5-20 % slower on this part until its clocks have adjusted to the
@@ -266,8 +272,6 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    base_mem = torch.cuda.memory_allocated()
-    torch.cuda.reset_peak_memory_stats()
 
     # timed region: events only around the streaming kernel (profile mode 2)
     _lib.check(lib.stk_profile_enable(2))
@@ -298,6 +302,26 @@ def main():
     breakdown = read_profile(("sample_kernel", "thr_kernel", "main_kernel", "merge_kernel", "group_kernel",
                               "cand_kernel"))
     _lib.check(lib.stk_profile_enable(0))
+
+    recall = None
+    if wl["op"] != "exact":
+        # recall@k of the approximate op (bench/run_recall.py:74-91 measures it
+        # against the dense reference), untimed, on this workload's own inputs
+        from streamtopk_sae import reference_topk_sae
+        from streamtopk_sae.utils import recall_per_row
+        _, I_ap = step()
+        _, I_ex = topk_sae_cuda_exact(X, W, b, k)
+        _, I_dense = reference_topk_sae(X, W, b, k)
+        r_ex, r_dense = recall_per_row(I_ap, I_ex), recall_per_row(I_ap, I_dense)
+        recall = {"recall_at_k_vs_exact": round(float(r_ex.mean()), 6),
+                  "min_row_vs_exact": round(float(r_ex.min()), 6),
+                  "recall_at_k_vs_dense_reference": round(float(r_dense.mean()), 6),
+                  "min_row_vs_dense_reference": round(float(r_dense.min()), 6),
+                  "rows": B, "k": k, "c": wl["c"],
+                  "note": "against topk_sae_cuda_exact and against reference_topk_sae (fp32 dense "
+                          "scores + torch.topk); the two references may differ on near-tied scores"}
+        del I_dense
+        torch.cuda.empty_cache()
 
     ms_per_step = 1e3 * wall / args.steps
     rows_per_s = B * args.steps / wall
@@ -355,7 +379,10 @@ def main():
                      "kernels_us": {n: round(v["avg_us"], 2) for n, v in breakdown.items()}},
         "device_settle": {"seconds": round(settle_s, 3), "steps": settle_steps,
                           "note": "untimed calls of the step before the warmup steps (sustained clocks)"},
-        "memory": {"peak_extra_bytes": int(peak_extra), "BxF_fp32_bytes": B * F * 4},
+        "memory": {"peak_extra_bytes": int(peak_extra), "BxF_fp32_bytes": B * F * 4,
+                   "note": "peak allocation over the resident inputs, from the first call on (the "
+                           "workspace the op keeps per stream, the outputs in flight)"},
+        **({"recall": recall} if recall is not None else {}),
         "reference_published": "A5000: ~60 rows/s on this config read off results/report/roofline.png "
                                "(not tabulated; BASELINE.json published is empty)",
     }

@@ -12,8 +12,14 @@ value descending.  The device ops run the gfx950 kernels of
 ``libstreamtopk_hip.so`` on the current stream of X's device; outputs and the
 workspace are allocated here with torch, so ``torch.cuda.max_memory_allocated``
 sees every byte and no (B, F) buffer is ever created.
+
+The workspace (scratch for the duration of one call) is kept per (device,
+stream) and reused by later calls on that stream, grown when a call needs more:
+calls queued on one stream run one after another, and calls on different
+streams get different workspaces.  ``clear_workspace_cache()`` releases them.
 """
 import ctypes
+import threading
 
 import torch
 
@@ -28,6 +34,31 @@ _DTYPES = {
 
 def _ptr(t):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+_WS = {}                      # (device index, stream handle) -> uint8 device tensor
+_WS_LOCK = threading.Lock()
+
+
+def _workspace(device, stream, nbytes):
+    """The workspace of `stream` on `device`, at least `nbytes` long.  A
+    smaller one is dropped first: the caching allocator hands its block out
+    again only in order on the same stream, after the calls queued on it."""
+    key = (device.index, int(stream))
+    with _WS_LOCK:
+        ws = _WS.get(key)
+        if ws is None or ws.numel() < nbytes:
+            _WS.pop(key, None)
+            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+            _WS[key] = ws
+        return ws
+
+
+def clear_workspace_cache():
+    """Release every cached workspace (the next call on each stream allocates
+    its own again)."""
+    with _WS_LOCK:
+        _WS.clear()
 
 
 def _pad_d(X, W_enc, multiple):
@@ -153,8 +184,8 @@ def exact_forward(X, W_enc, b_enc, k, f_offset=0):
         _lib.check(lib.stk_exact_workspace_bytes(B, d, F, k, dt, ctypes.byref(nbytes)))
         V = torch.empty((B, k), dtype=torch.float32, device=X.device)
         I = torch.empty((B, k), dtype=torch.int32, device=X.device)
-        ws = torch.empty(max(nbytes.value, 1), dtype=torch.uint8, device=X.device)
         stream = torch.cuda.current_stream(X.device).cuda_stream
+        ws = _workspace(X.device, stream, nbytes.value)
         if f_offset:
             rc = lib.stk_exact_forward_shard(_ptr(X), _ptr(W_enc), _ptr(b_enc), _ptr(V), _ptr(I),
                                              B, d, F, k, dt, int(f_offset), _ptr(ws), ws.numel(),
@@ -210,8 +241,8 @@ def merge_topk_shards(values, indices, k):
         _lib.check(lib.stk_topk_merge_workspace_bytes(B, k, nparts, ctypes.byref(nbytes)))
         V = torch.empty((B, k), dtype=torch.float32, device=Vp.device)
         I = torch.empty((B, k), dtype=torch.int32, device=Vp.device)
-        ws = torch.empty(max(nbytes.value, 1), dtype=torch.uint8, device=Vp.device)
         stream = torch.cuda.current_stream(Vp.device).cuda_stream
+        ws = _workspace(Vp.device, stream, nbytes.value)
         _lib.check(lib.stk_topk_merge(_ptr(Vp), _ptr(Ip), nparts, B, k, _ptr(V), _ptr(I),
                                       _ptr(ws), ws.numel(), ctypes.c_void_p(stream)))
     return V, I
@@ -252,8 +283,8 @@ def approx_forward(X, W_enc, b_enc, k, c, candidate_buffer=None, candidates=Fals
                                                   ctypes.byref(nbytes)))
         V = torch.empty((B, k), dtype=torch.float32, device=X.device)
         I = torch.empty((B, k), dtype=torch.int32, device=X.device)
-        ws = torch.empty(max(nbytes.value, 1), dtype=torch.uint8, device=X.device)
         stream = torch.cuda.current_stream(X.device).cuda_stream
+        ws = _workspace(X.device, stream, nbytes.value)
         rc = lib.stk_approx_forward(_ptr(X), _ptr(W_enc), _ptr(b_enc), _ptr(V), _ptr(I),
                                     B, d, F, k, c, dt, _ptr(cand_vals), _ptr(cand_idxs),
                                     _ptr(ws), ws.numel(), ctypes.c_void_p(stream))
