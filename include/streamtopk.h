@@ -58,8 +58,11 @@ int stk_exact_workspace_bytes(int64_t B, int64_t d, int64_t F, int64_t k, int dt
  * Replaces streamtopk_cuda_exact_forward (streamtopk_exact.cu:788-833),
  * bound in the reference at bindings.cpp:33 and called from ops.py:57.
  * k must be one of 1,2,4,8,16,32,64,128 and <= F; d <= 4096; d must be a
- * multiple of 64 (fp16/bf16) or 32 (fp32): one 128-byte d-step of a row (the
- * Python op zero-pads other d). */
+ * multiple of 8 (fp16/bf16) or 4 (fp32), so that rows are 16-byte aligned (the
+ * kernels mask a partial last 128-byte d-step; the Python op zero-pads other
+ * d).  If a streaming kernel ever exhausted its bounded spill-and-retry loop
+ * (which its bounds rule out), every output row is marked instead of being
+ * returned short: indices -1, values NaN. */
 int stk_exact_forward(const void* X, const void* W, const float* b, float* V, int32_t* I,
                       int64_t B, int64_t d, int64_t F, int64_t k, int dtype,
                       void* workspace, size_t workspace_bytes, void* stream);
