@@ -434,6 +434,7 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     mg.k = (int)k;
     mg.f_offset = (int32_t)f_offset;
     mg.err = err;
+    mg.ties = 0;   // one encode's keys are distinct
     mg.V = V; mg.I = I;
     const int pg = prof_begin("merge_kernel", st);
     e = launch_merge(mg, B, st);
@@ -669,6 +670,7 @@ int stk_topk_merge(const float* Vp, const int32_t* Ip, int64_t nparts, int64_t B
     mg.k = (int)k;
     mg.f_offset = 0;
     mg.err = nullptr;
+    mg.ties = 1;   // the parts may repeat a latent
     mg.V = V; mg.I = I;
     const int pg = prof_begin("merge_kernel", st);
     e = launch_merge(mg, B, st);

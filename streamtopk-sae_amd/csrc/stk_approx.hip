@@ -374,7 +374,7 @@ __global__ __launch_bounds__(kThreads) void cand_kernel(CandArgs a)
     const int mk = n < k ? n : k;
     if (tid < mk) {
         const uint64_t key = S.buf[tid];
-        const int r = rank_desc(S, mk, key);
+        const int r = rank_desc<false>(S, mk, key, tid);
         a.V[row * k + r] = key_value(key);
         a.I[row * k + r] = key_index(key);
     }

@@ -169,6 +169,8 @@ struct MergeArgs {
                                  //   3, 4: merge_seg_kernel (head <= 256 keys, one
                                  //   segment per thread; 30 or 62 keys per pass)
     int32_t f_offset;            // added to every emitted index (a shard's first latent)
+    int ties;                    // non-zero: keys may repeat (stk_topk_merge's parts); equal keys
+                                 //   take consecutive ranks
     const uint32_t* err;         // non-zero: mark the output rows (-1, NaN); may be null
     float* V;
     int32_t* I;

@@ -50,21 +50,17 @@ __device__ __forceinline__ float pick16(const f32x16& v, uint32_t r)
 // ---------------------------------------------------------------------------
 // main_kernel
 // ---------------------------------------------------------------------------
-// Spills LDS queues among this wave's rows (wave*R .. wave*R+R-1) to their
-// global segments (row r's at seg + r * seg_stride, cap keys): the full ones,
-// or with `all` every non-empty one.  A segment without room for the queue's
-// keys is first rank-compacted to its top k (raising the row threshold), then
-// the LDS keys above the threshold are appended.  Every global access of a
-// row is made by the wave that owns the row.  Ends with the wave's stores
-// complete.
+// Spills the LDS queues of the rows `sel` selects among this wave's rows (bit
+// i: row wave*R + i) to their global segments (row r's at seg + r *
+// seg_stride, cap keys).  A segment without room for the queue's keys is
+// first rank-compacted to its top k (raising the row threshold), then the LDS
+// keys above the threshold are appended.  Every global access of a row is
+// made by the wave that owns the row.  Ends with the wave's stores complete.
 template <int R>
-__device__ __forceinline__ void spill_rows(int* cnt, int* gcnt, uint64_t* thr, const uint64_t* lqk,
-                                           uint64_t* seg, int64_t seg_stride, uint64_t* scr, int lq, int cap,
-                                           int k, int wave, int lane, bool all)
+__device__ __forceinline__ void spill_sel(uint64_t full, int* cnt, int* gcnt, uint64_t* thr, const uint64_t* lqk,
+                                          uint64_t* seg, int64_t seg_stride, uint64_t* scr, int lq, int cap,
+                                          int k, int wave, int lane)
 {
-    const int myrow = wave * R + (lane < R ? lane : 0);
-    const int mycnt = cnt[myrow];
-    uint64_t full = __ballot(lane < R && (all ? mycnt > 0 : mycnt >= lq));
     while (full) {
         const int i = __builtin_ctzll(full);
         full &= full - 1;
@@ -90,6 +86,54 @@ __device__ __forceinline__ void spill_rows(int* cnt, int* gcnt, uint64_t* thr, c
             cnt[row] = 0;
         }
         __builtin_amdgcn_wave_barrier();
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the segment stores are complete
+}
+
+// spill_sel over this wave's full queues.
+template <int R>
+__device__ __forceinline__ void spill_rows(int* cnt, int* gcnt, uint64_t* thr, const uint64_t* lqk,
+                                           uint64_t* seg, int64_t seg_stride, uint64_t* scr, int lq, int cap,
+                                           int k, int wave, int lane)
+{
+    const int myrow = wave * R + (lane < R ? lane : 0);
+    const uint64_t full = __ballot(lane < R && cnt[myrow] >= lq);
+    spill_sel<R>(full, cnt, gcnt, thr, lqk, seg, seg_stride, scr, lq, cap, k, wave, lane);
+}
+
+// End of main_kernel: moves the LDS queue keys of this wave's rows into their
+// segments.  Rows whose segment lacks room go through spill_sel (compacted
+// first); the others' keys are copied as they are, one row per round with a
+// key per lane and no round waiting for another (a queued key at or below
+// the final threshold is only an extra candidate, which the merge drops).
+// Afterwards gcnt holds each segment's key count.  Ends with the stores
+// complete.
+template <int R>
+__device__ __forceinline__ void flush_rows(int* cnt, int* gcnt, uint64_t* thr, const uint64_t* lqk,
+                                           uint64_t* seg, int64_t seg_stride, uint64_t* scr, int lq, int cap,
+                                           int k, int wave, int lane)
+{
+    const int myrow = wave * R + (lane < R ? lane : 0);
+    int c = lane < R ? (cnt[myrow] < lq ? cnt[myrow] : lq) : 0;
+    int g = lane < R ? gcnt[myrow] : 0;
+    const uint64_t tight = __ballot(c > 0 && g + c > cap);
+    if (tight) {
+        spill_sel<R>(tight, cnt, gcnt, thr, lqk, seg, seg_stride, scr, lq, cap, k, wave, lane);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        c = lane < R ? (cnt[myrow] < lq ? cnt[myrow] : lq) : 0;   // 0 for the rows just spilled
+        g = lane < R ? gcnt[myrow] : 0;
+    }
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int ci = __shfl(c, i), gi = __shfl(g, i);
+        const int row = wave * R + i;
+        if (lane < ci) seg[row * seg_stride + gi + lane] = lqk[row * lq + lane];   // lq <= 64
+    }
+    if (lane < R) {
+        gcnt[myrow] = g + c;
+        cnt[myrow] = 0;
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the segment stores are complete
 }
@@ -221,7 +265,7 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
                 break;
             }
             __syncthreads();   // the LDS queues are complete
-            spill_rows<R>(cnt, gcnt, thr, lqk, seg, a.list_cap, cscr + wave * cap, lq, cap, k, wave, lane, false);
+            spill_rows<R>(cnt, gcnt, thr, lqk, seg, a.list_cap, cscr + wave * cap, lq, cap, k, wave, lane);
             __syncthreads();
             // drop pending scores that fell below a raised threshold
 #pragma unroll
@@ -241,7 +285,10 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
     // segments (compacting a segment without room), then publishes how many
     // keys each of its segments holds ----
     __syncthreads();
-    spill_rows<R>(cnt, gcnt, thr, lqk, seg, a.list_cap, cscr + wave * cap, lq, cap, k, wave, lane, true);
+    flush_rows<R>(cnt, gcnt, thr, lqk, seg, a.list_cap, cscr + wave * cap, lq, cap, k, wave, lane);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const int myrow = wave * R + lane;
     if (lane < R && b0 + myrow < B) a.seg_cnt[(b0 + myrow) * gridDim.x + blockIdx.x] = gcnt[myrow];
 }
@@ -405,16 +452,38 @@ __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
     auto item = [&](int t) { return 4 * tid + kThreads * 4 * (t >> 2) + (t & 3); };
     const float* prow = a.P + row * a.p_row;
     const int64_t split_stride = a.p_split;
-    f32x4 v[kQuads];
+    // The bias of the sampled latents goes out first (it does not depend on
+    // P), then the splits' partial sums kSplitBatch splits at a time with all
+    // their loads in flight; the sums are added in split order, then the bias.
+    constexpr int kSplitBatch = 4;
+    float bsv[kItems];
+    if (a.bias != nullptr) {
 #pragma unroll
-    for (int u = 0; u < kQuads; ++u) v[u] = *(const f32x4*)(prow + item(4 * u));
-    for (int sp = 1; sp < a.nsplit; ++sp) {
+        for (int t = 0; t < kItems; ++t) bsv[t] = a.bias[sample_latent(item(t), a.samp_log2)];   // 4-byte aligned only
+    } else {
 #pragma unroll
-        for (int u = 0; u < kQuads; ++u) v[u] += *(const f32x4*)(prow + sp * split_stride + item(4 * u));
+        for (int t = 0; t < kItems; ++t) bsv[t] = 0.f;
     }
-    if (a.bias != nullptr) {   // only 4-byte aligned: scalar loads
+    f32x4 v[kQuads];
+    for (int sp0 = 0; sp0 < a.nsplit; sp0 += kSplitBatch) {
+        f32x4 p[kSplitBatch][kQuads];
 #pragma unroll
-        for (int t = 0; t < kItems; ++t) v[t >> 2][t & 3] += a.bias[sample_latent(item(t), a.samp_log2)];
+        for (int j = 0; j < kSplitBatch; ++j) {
+            const int sp = sp0 + j < a.nsplit ? sp0 + j : sp0;   // past the last split: reloaded, not added
+#pragma unroll
+            for (int u = 0; u < kQuads; ++u) p[j][u] = *(const f32x4*)(prow + sp * split_stride + item(4 * u));
+        }
+#pragma unroll
+        for (int j = 0; j < kSplitBatch; ++j) {
+            if (sp0 + j < a.nsplit) {
+#pragma unroll
+                for (int u = 0; u < kQuads; ++u) v[u] = (sp0 + j == 0) ? p[j][u] : v[u] + p[j][u];
+            }
+        }
+    }
+    if (a.bias != nullptr) {
+#pragma unroll
+        for (int t = 0; t < kItems; ++t) v[t >> 2][t & 3] += bsv[t];
     }
     uint64_t key[kItems];
     uint64_t m = 0;
@@ -443,10 +512,14 @@ __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
     uint64_t T = T0;
     uint64_t* out = a.list_keys + row * a.list_cap;
     if (n <= kThreads) {
-        // the sample's k largest keys, sorted: the k-th is the threshold
-        const uint64_t v = bitonic_desc(S, tid < n ? S.buf[tid] : 0ull, tid);
-        if (tid == a.k - 1) S.thr = v;
-        if (tid < a.k) out[tid] = v;
+        // the sample's k largest keys by rank, counted (thread t ranks key
+        // t): the key of rank k - 1 is the threshold
+        if (tid < n) {
+            const uint64_t key = S.buf[tid];
+            const int r = rank_desc<false>(S, n, key, tid);
+            if (r < a.k) out[r] = key;
+            if (r == a.k - 1) S.thr = key;
+        }
         if (tid == 0) S.sel_cnt = a.k;
         __syncthreads();
         T = S.thr;
@@ -631,10 +704,14 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
         }
         merge_pass(S, v, k, tid, run);
     }
-    emit_topk(S, k, tid, [&](int r, uint64_t kk) {
+    auto out = [&](int r, uint64_t kk) {
         a.V[row * k + r] = key_value(kk);
         a.I[row * k + r] = key_index(kk) + a.f_offset;
-    });
+    };
+    if (a.ties)
+        emit_topk<true>(S, k, tid, out);
+    else
+        emit_topk<false>(S, k, tid, out);
 }
 
 // Per row: top-k of main_kernel's list -- a head of at most kThreads keys,

@@ -1,7 +1,7 @@
 // stk_select.h -- workgroup-wide top-k selection over 64-bit sort keys held in
-// LDS (radix select by 8-bit digits, most significant first), the bitonic sort
-// that emits the final k keys in descending order, and slot reservation with
-// one LDS atomic per wave.
+// LDS (radix select by 8-bit digits, most significant first), ranking by
+// counting that emits the final k keys in descending order, and slot
+// reservation with one LDS atomic per wave.
 #pragma once
 #include "stk_device.h"
 
@@ -181,39 +181,14 @@ __device__ inline void select_compact(SelShared& S, int n, int k, int tid)
     __syncthreads();
 }
 
-// Bitonic sort of one key per thread (kThreads keys, padding 0) into
-// descending order: returns the key of rank tid.  Compare-exchange partners
-// closer than a wave apart are reached by lane shuffles; the three farther
-// stages go through S.tmax, with barriers.  Every thread must take part.
-__device__ inline uint64_t bitonic_desc(SelShared& S, uint64_t v, int tid)
-{
-#pragma unroll
-    for (int size = 2; size <= kThreads; size <<= 1) {
-#pragma unroll
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            uint64_t o;
-            if (stride >= 64) {
-                __syncthreads();
-                S.tmax[tid] = v;
-                __syncthreads();
-                o = S.tmax[tid ^ stride];
-            } else {
-                const uint32_t lo = __shfl_xor((uint32_t)v, stride, 64);
-                const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), stride, 64);
-                o = ((uint64_t)hi << 32) | lo;
-            }
-            // blocks of `size` alternate direction; the final one is descending
-            const bool desc = (tid & size) == 0;
-            const bool lower = (tid & stride) == 0;
-            v = (lower == desc) ? (o > v ? o : v) : (o < v ? o : v);
-        }
-    }
-    __syncthreads();   // S.tmax free again
-    return v;
-}
-
-// Rank of `key` among buf[0..n) in descending key order (keys are unique).
-__device__ inline int rank_desc(const SelShared& S, int n, uint64_t key)
+// Rank of buf[pos] = `key` among buf[0..n) in descending key order: the
+// number of larger keys.  Keys hold their latent index, so the keys of one
+// encode are distinct; kTies also counts the equal keys at lower positions,
+// which keeps the ranks a permutation when a caller's keys repeat (shard
+// results merged by stk_topk_merge).  Every thread reads the same LDS words
+// (broadcast), 16 keys per round.
+template <bool kTies>
+__device__ inline int rank_desc(const SelShared& S, int n, uint64_t key, int pos)
 {
     int r = 0;
     int i = 0;
@@ -222,15 +197,24 @@ __device__ inline int rank_desc(const SelShared& S, int n, uint64_t key)
 #pragma unroll
         for (int u = 0; u < 8; ++u) v[u] = *(const u64x2*)(S.buf + i + 2 * u);
 #pragma unroll
-        for (int u = 0; u < 8; ++u) r += (int)(v[u][0] > key) + (int)(v[u][1] > key);
+        for (int u = 0; u < 8; ++u) {
+            if (kTies) {
+                r += (int)(v[u][0] > key || (v[u][0] == key && i + 2 * u < pos)) +
+                     (int)(v[u][1] > key || (v[u][1] == key && i + 2 * u + 1 < pos));
+            } else {
+                r += (int)(v[u][0] > key) + (int)(v[u][1] > key);
+            }
+        }
     }
-    for (; i < n; ++i) r += (int)(S.buf[i] > key);
+    for (; i < n; ++i) r += (int)(S.buf[i] > key || (kTies && S.buf[i] == key && i < pos));
     return r;
 }
 
 // Reduces buf[0..cnt) to its top k and calls emit(rank, key) for rank < k,
-// rank 0 being the largest.  Returns the number of keys emitted.
-template <class Emit>
+// rank 0 being the largest.  Up to kThreads keys are ranked directly by
+// counting (thread t ranks key t), more are first reduced to the k largest by
+// radix selection.  Returns the number of keys emitted.
+template <bool kTies = false, class Emit>
 __device__ inline int emit_topk(SelShared& S, int k, int tid, Emit emit)
 {
     __syncthreads();
@@ -239,11 +223,12 @@ __device__ inline int emit_topk(SelShared& S, int k, int tid, Emit emit)
         select_compact(S, n, k, tid);   // k <= kMaxK <= kThreads keys remain
         n = k;
     }
-    __syncthreads();
-    const uint64_t v = bitonic_desc(S, tid < n ? S.buf[tid] : 0ull, tid);
-    const int m = n < k ? n : k;
-    if (tid < m) emit(tid, v);
-    return m;
+    if (tid < n) {
+        const uint64_t key = S.buf[tid];
+        const int r = rank_desc<kTies>(S, n, key, tid);
+        if (r < k) emit(r, key);
+    }
+    return n < k ? n : k;
 }
 
 }  // namespace stk

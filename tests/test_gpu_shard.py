@@ -97,3 +97,16 @@ def test_shard_offset_beyond_int32_rejected(cuda_dev):
     X, W, b = make_inputs(4, 64, 256, torch.bfloat16, seed=0, device=cuda_dev)
     with pytest.raises(RuntimeError, match="int32 index range"):
         topk_sae_cuda_exact(X, W, b, 8, f_offset=2**31 - 100)
+
+
+def test_merge_repeated_parts_keep_every_copy(cuda_dev):
+    """Parts that repeat a latent (the same shard passed twice) give equal keys;
+    they take consecutive ranks, so every output slot is written: each of the
+    top k/2 latents appears twice, in order."""
+    X, W, b = make_inputs(16, 256, 8192, torch.bfloat16, seed=4, device=cuda_dev)
+    V, I = topk_sae_cuda_exact(X, W, b, 32)
+    V2, I2 = merge_topk_shards([V, V], [I, I], 32)
+    torch.cuda.synchronize()
+    want_v = V[:, :16].repeat_interleave(2, dim=1)
+    want_i = I[:, :16].repeat_interleave(2, dim=1)
+    assert torch.equal(V2, want_v) and torch.equal(I2, want_i)
