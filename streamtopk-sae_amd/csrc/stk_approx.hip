@@ -147,6 +147,103 @@ __device__ __forceinline__ void bitonic_topc(T (&v)[8], int l)
     if constexpr (C < 128) bitonic_topc_merge<C>(v, l);
 }
 
+// Sorts one (row, group) segment of a staged 32-row block: the wave's 16-lane
+// row l = lane % 16 takes the 128 staged words of block row rl, group g
+// (latents 128 g .. of tile `tile`), sorts them in registers (8 per lane)
+// and writes the group's top-c, descending, padded with (-FLT_MAX, -1) past
+// the end of F, for output row rowblk + rl (streamtopk_approx.cu:118-166).
+// Every lane of the wave takes part.
+template <int C>
+__device__ __forceinline__ void sort_segment(const GroupArgs& a, const uint32_t* ordv, int rl, int g, int l,
+                                             int64_t rowblk, int64_t tile)
+{
+    constexpr int c = C;
+    const int64_t B = a.B, G = a.num_groups;
+    const int64_t f0 = tile * kGroupTile;
+    const uint32_t* src = ordv + rl * kOrdStride + g * kApproxGroup;
+    const u32x4 w0 = *(const u32x4*)(src + 8 * l), w1 = *(const u32x4*)(src + 8 * l + 4);
+    // Short keys: the ordered word with its low 7 bits replaced by
+    // 127 - position, so equal truncated words go to the lower
+    // position; padding (word 0) sorts last.  Entries with equal
+    // truncated words end up adjacent, so unless two such real
+    // entries meet within the first c + 1, the short order is the
+    // exact one.
+    uint32_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        v[j] = ((j < 4 ? w0[j] : w1[j - 4]) & ~0x7Fu) | (uint32_t)(127 - (8 * l + j));
+    // c < 128: only the top c are selected and ordered (entries c ..
+    // 127 end up holding copies); c = 128: the full sort
+    bitonic_topc<C>(v, l);
+    const uint32_t nx = __shfl_down(v[0], 1, 16);   // entry 8l + 8
+    bool tie = false;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t y = j < 7 ? v[j + 1] : nx;
+        tie |= 8 * l + j < c - 1 && (y >> 7) != 0 && (v[j] >> 7) == (y >> 7);
+    }
+    if constexpr (C < 128) {
+        // the (c+1)-th is not at hand: a real entry outside the top c
+        // whose truncated word equals the c-th's shows as more than c
+        // real entries at or above that word
+        const uint32_t tc = __shfl(v[7], c / 8 - 1, 16) >> 7;   // entry c - 1
+        int above = 0;
+        // the words again from LDS, rather than held through the network
+        const u32x4 r0 = *(const u32x4*)(src + 8 * l), r1 = *(const u32x4*)(src + 8 * l + 4);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t ov = j < 4 ? r0[j] : r1[j - 4];
+            above += (ov != 0u && (ov >> 7) >= tc) ? 1 : 0;
+        }
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1) above += __shfl_xor(above, m, 16);
+        tie |= tc != 0u && above != c;
+    }
+    float val[8];
+    uint32_t idx[8];
+    const uint32_t fg = (uint32_t)(f0 + g * kApproxGroup);
+    if (__ballot(tie) == 0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t pos = 127u - (v[j] & 0x7Fu);
+            const bool real = (v[j] >> 7) != 0;
+            val[j] = real ? key_value((uint64_t)src[pos] << 32) : -3.402823466e+38f;
+            idx[j] = real ? fg + pos : 0xFFFFFFFFu;
+        }
+    } else {
+        // full keys for this wave's four segments
+        uint64_t u[8];
+        const u32x4 r0 = *(const u32x4*)(src + 8 * l), r1 = *(const u32x4*)(src + 8 * l + 4);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t ov = j < 4 ? r0[j] : r1[j - 4];
+            u[j] = ov ? (((uint64_t)ov << 32) | (0xFFFFFFFFu - (fg + 8 * l + j))) : 0ull;
+        }
+        bitonic_sort128(u, l);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            val[j] = u[j] ? key_value(u[j]) : -3.402823466e+38f;
+            idx[j] = u[j] ? (uint32_t)key_index(u[j]) : 0xFFFFFFFFu;
+        }
+    }
+    const int64_t row = rowblk + rl;
+    const int64_t grp = 2 * tile + g;
+    if (row < B && grp < G && 8 * l < c) {
+        // the block's uniform part, then this lane's, recomputed at
+        // every store (the empty asm hides rl's invariance: hoisted,
+        // the 64-bit lane offsets of every block would be held in
+        // registers through the tile loop, and spilled)
+        const int64_t ob = (rowblk * G + 2 * tile) * c;
+        int rlv = rl;
+        asm volatile("" : "+v"(rlv));
+        const int64_t o = ob + ((int64_t)rlv * G + g) * c + 8 * l;
+        *(f32x4*)(a.cand_vals + o) = f32x4{val[0], val[1], val[2], val[3]};
+        *(f32x4*)(a.cand_vals + o + 4) = f32x4{val[4], val[5], val[6], val[7]};
+        *(u32x4*)(a.cand_idxs + o) = u32x4{idx[0], idx[1], idx[2], idx[3]};
+        *(u32x4*)(a.cand_idxs + o + 4) = u32x4{idx[4], idx[5], idx[6], idx[7]};
+    }
+}
+
 template <int DT, int NB, int C>
 __global__ __launch_bounds__(kMainThreads, 1) void group_kernel(GroupArgs a)
 {
@@ -161,7 +258,6 @@ __global__ __launch_bounds__(kMainThreads, 1) void group_kernel(GroupArgs a)
     const int l = lane & 15, sq = lane >> 4;
     const int64_t b0 = (int64_t)blockIdx.y * (32 * NB);
     const int64_t B = a.B, F = a.F, G = a.num_groups;
-    constexpr int c = C;   // a.c
     const int64_t num_tiles = (G + 1) / 2;
 
     TS ts;
@@ -209,88 +305,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void group_kernel(GroupArgs a)
             for (int rd = 0; rd < 2; ++rd) {
                 const int seg = wave * 8 + rd * 4 + sq;
                 const int rl = seg >> 1, g = seg & 1;
-                const uint32_t* src = ordv + rl * kOrdStride + g * kApproxGroup;
-                const u32x4 w0 = *(const u32x4*)(src + 8 * l), w1 = *(const u32x4*)(src + 8 * l + 4);
-                // Short keys: the ordered word with its low 7 bits replaced by
-                // 127 - position, so equal truncated words go to the lower
-                // position; padding (word 0) sorts last.  Entries with equal
-                // truncated words end up adjacent, so unless two such real
-                // entries meet within the first c + 1, the short order is the
-                // exact one.
-                uint32_t v[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    v[j] = ((j < 4 ? w0[j] : w1[j - 4]) & ~0x7Fu) | (uint32_t)(127 - (8 * l + j));
-                // c < 128: only the top c are selected and ordered (entries c ..
-                // 127 end up holding copies); c = 128: the full sort
-                bitonic_topc<C>(v, l);
-                const uint32_t nx = __shfl_down(v[0], 1, 16);   // entry 8l + 8
-                bool tie = false;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const uint32_t y = j < 7 ? v[j + 1] : nx;
-                    tie |= 8 * l + j < c - 1 && (y >> 7) != 0 && (v[j] >> 7) == (y >> 7);
-                }
-                if constexpr (C < 128) {
-                    // the (c+1)-th is not at hand: a real entry outside the top c
-                    // whose truncated word equals the c-th's shows as more than c
-                    // real entries at or above that word
-                    const uint32_t tc = __shfl(v[7], c / 8 - 1, 16) >> 7;   // entry c - 1
-                    int above = 0;
-                    // the words again from LDS, rather than held through the network
-                    const u32x4 r0 = *(const u32x4*)(src + 8 * l), r1 = *(const u32x4*)(src + 8 * l + 4);
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const uint32_t ov = j < 4 ? r0[j] : r1[j - 4];
-                        above += (ov != 0u && (ov >> 7) >= tc) ? 1 : 0;
-                    }
-#pragma unroll
-                    for (int m = 1; m < 16; m <<= 1) above += __shfl_xor(above, m, 16);
-                    tie |= tc != 0u && above != c;
-                }
-                float val[8];
-                uint32_t idx[8];
-                const uint32_t fg = (uint32_t)(f0 + g * kApproxGroup);
-                if (__ballot(tie) == 0) {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const uint32_t pos = 127u - (v[j] & 0x7Fu);
-                        const bool real = (v[j] >> 7) != 0;
-                        val[j] = real ? key_value((uint64_t)src[pos] << 32) : -3.402823466e+38f;
-                        idx[j] = real ? fg + pos : 0xFFFFFFFFu;
-                    }
-                } else {
-                    // full keys for this wave's four segments
-                    uint64_t u[8];
-                    const u32x4 r0 = *(const u32x4*)(src + 8 * l), r1 = *(const u32x4*)(src + 8 * l + 4);
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const uint32_t ov = j < 4 ? r0[j] : r1[j - 4];
-                        u[j] = ov ? (((uint64_t)ov << 32) | (0xFFFFFFFFu - (fg + 8 * l + j))) : 0ull;
-                    }
-                    bitonic_sort128(u, l);
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        val[j] = u[j] ? key_value(u[j]) : -3.402823466e+38f;
-                        idx[j] = u[j] ? (uint32_t)key_index(u[j]) : 0xFFFFFFFFu;
-                    }
-                }
-                const int64_t row = b0 + 32 * n + rl;
-                const int64_t grp = 2 * tile + g;
-                if (row < B && grp < G && 8 * l < c) {
-                    // the block's uniform part, then this lane's, recomputed at
-                    // every store (the empty asm hides rl's invariance: hoisted,
-                    // the 64-bit lane offsets of every block would be held in
-                    // registers through the tile loop, and spilled)
-                    const int64_t ob = ((b0 + 32 * n) * G + 2 * tile) * c;
-                    int rlv = rl;
-                    asm volatile("" : "+v"(rlv));
-                    const int64_t o = ob + ((int64_t)rlv * G + g) * c + 8 * l;
-                    *(f32x4*)(a.cand_vals + o) = f32x4{val[0], val[1], val[2], val[3]};
-                    *(f32x4*)(a.cand_vals + o + 4) = f32x4{val[4], val[5], val[6], val[7]};
-                    *(u32x4*)(a.cand_idxs + o) = u32x4{idx[0], idx[1], idx[2], idx[3]};
-                    *(u32x4*)(a.cand_idxs + o + 4) = u32x4{idx[4], idx[5], idx[6], idx[7]};
-                }
+                sort_segment<C>(a, ordv, rl, g, l, b0 + 32 * n, tile);
             }
         }
     });

@@ -74,6 +74,34 @@ __device__ __forceinline__ uint64_t make_key(float v, int64_t idx)
     return ((uint64_t)ordered_u32(v) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)idx);
 }
 
+// Buffer resource (raw, gfx9 family): loads at byte offsets >= num_records
+// return zeros, which bounds rows past B and latents past F, and a zero-length
+// resource makes whole steps read as zeros.
+// The streaming kernels build every resource uniform over the wave; its fields
+// go through readfirstlane so that the compiler keeps it in scalar registers
+// whatever its uniformity analysis concludes (a resource it takes for
+// divergent costs a waterfall loop around every load).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t num_records)
+{
+    const uint64_t b = (uint64_t)base;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    const int n = __builtin_amdgcn_readfirstlane((int)num_records);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, n, 0x00020000);
+}
+
+// LDS loads (global -> LDS, no registers): lane i of one instruction writes
+// the 16 bytes at ldsbase + 16*i.
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, unsigned char* ldsbase, int voff, int soff)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)ldsbase, 16, voff, soff, 0, 0);
+}
+
+// Ring layout: row r's 16-byte chunk c sits in slot c ^ ((r >> 1) & 7) of the
+// row's 128 bytes, so that the MFMA-layout reads (32 rows x one chunk per
+// half-wave) hit 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int xswz(int r) { return (r >> 1) & 7; }
+
 // ---------------------------------------------------------------------------
 // One quad (16 bytes of W for this lane x 16 bytes of X) through the MFMA.
 // ---------------------------------------------------------------------------

@@ -53,34 +53,6 @@ constexpr int kLWStage = kLTile * kStepBytes;               // W ring stage: 256
 constexpr int kLXStage = kLargeRows * kStepBytes;           // X ring stage: 256 rows x 128 B (swizzled)
 constexpr int kLXChunks = kLargeRows * 8 / kLargeThreads;  // 16-byte X chunks per thread per d-step
 
-// Buffer resource (raw, gfx9 family): loads at byte offsets >= num_records
-// return zeros, which bounds rows past B and latents past F, and a zero-length
-// resource makes whole steps read as zeros.
-// Every resource of this file is uniform over the wave; its fields go through
-// readfirstlane so that the compiler keeps it in scalar registers whatever
-// its uniformity analysis concludes (a resource it takes for divergent costs
-// a waterfall loop around every load).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t num_records)
-{
-    const uint64_t b = (uint64_t)base;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
-    const int n = __builtin_amdgcn_readfirstlane((int)num_records);
-    return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, n, 0x00020000);
-}
-
-// LDS loads (global -> LDS, no registers): lane i of one instruction writes
-// the 16 bytes at ldsbase + 16*i.
-__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, unsigned char* ldsbase, int voff, int soff)
-{
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)ldsbase, 16, voff, soff, 0, 0);
-}
-
-// Ring layout: row r's 16-byte chunk c sits in slot c ^ ((r >> 1) & 7) of the
-// row's 128 bytes, so that the MFMA-layout reads (32 rows x one chunk per
-// half-wave) hit 16 distinct 16-byte bank groups.
-__device__ __forceinline__ int xswz(int r) { return (r >> 1) & 7; }
-
 typedef __attribute__((address_space(1))) uint64_t gu64;   // a key in global memory
 
 // Calls f(std::integral_constant<int, i>) for i = 0 .. N-1 (compile-time i, so

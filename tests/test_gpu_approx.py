@@ -158,3 +158,36 @@ def test_approx_candidates_equal_scores(cuda_dev):
     V, I = topk_sae_cuda_approx(X, W, b, k, c, candidate_buffer=cb)
     assert torch.equal(I.cpu(), torch.arange(k, dtype=torch.int32).expand(B, k))
     assert bool((V == 0.5).all()) and bool((cb == 0.5).all())
+
+
+@pytest.mark.parametrize("dtype,B,d,F", [
+    (torch.bfloat16, 128, 200, 150000),   # ragged last d-step; 3 tiles per workgroup, the last one 1
+    (torch.bfloat16, 128, 256, 200000),   # 4 tiles per workgroup, the last one 2
+    (torch.float32, 160, 36, 70000),      # fp32, a partial second d-step; a partial second row block
+    (torch.float16, 128, 64, 3000),       # one d-step: every tile's sort takes extra intervals
+])
+def test_candidates_full_row_blocks(cuda_dev, dtype, B, d, F):
+    """Full 128-row blocks (four 32-row blocks per workgroup) with several tiles
+    per workgroup (odd and even counts), ragged and one-step d, every dtype:
+    per-group candidates against the oracle's, and the final top-k against f64
+    scores."""
+    print(f"case candidates full row blocks {dtype} B={B} d={d} F={F}", flush=True)
+    c, k = 32, 16
+    tol = 1e-5 if dtype == torch.float32 else 2e-3
+    X, W, b = make_inputs(B, d, F, dtype, seed=31, device=cuda_dev)
+    nt = (F + 127) // 128
+    cb = torch.empty((B, nt, c), dtype=torch.float32, device=cuda_dev)
+    V, I = topk_sae_cuda_approx(X, W, b, k, c, candidate_buffer=cb)
+    _, _, cvo, cio = oracle.approx(_np(X), _np(W), _np(b), k, c, with_candidates=True)
+    cbn = cb.cpu().numpy()
+    pad = cio < 0
+    assert np.array_equal(cbn[pad], cvo[pad])
+    err = np.abs(cbn[~pad] - cvo[~pad]) / np.maximum(np.abs(cvo[~pad]), 1.0)
+    assert err.max() <= tol
+    assert np.all(np.diff(cbn, axis=2) <= 0)
+    # the final top-k against f64 scores on a row subset (the exact kernel
+    # scores sampled latents through summed d-splits, so its values can differ
+    # from these in the last bit once F is large enough to be sampled)
+    rows = slice(0, 16)
+    S = oracle.scores_f64(_np(X[rows]), _np(W), _np(b))
+    check_against_scores(V[rows].cpu().numpy(), I[rows].cpu().numpy(), S, k, tol, "full row blocks")
