@@ -452,17 +452,23 @@ __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
     auto item = [&](int t) { return 4 * tid + kThreads * 4 * (t >> 2) + (t & 3); };
     const float* prow = a.P + row * a.p_row;
     const int64_t split_stride = a.p_split;
-    // The bias of the sampled latents goes out first (it does not depend on
-    // P), then the splits' partial sums kSplitBatch splits at a time with all
-    // their loads in flight; the sums are added in split order, then the bias.
-    constexpr int kSplitBatch = 4;
-    float bsv[kItems];
-    if (a.bias != nullptr) {
+    // With 16 items per thread the bias of the sampled latents goes out first
+    // (it does not depend on P) and the splits' partial sums four splits at a
+    // time with all their loads in flight; with 32 items (the larger sample),
+    // whose keys fill the registers, one split at a time and the bias last, as
+    // more loads in flight would cost occupancy.  Either way the sums are added
+    // in split order, then the bias.
+    constexpr bool kEarly = kItems <= 16;
+    constexpr int kSplitBatch = kEarly ? 4 : 1;
+    float bsv[kEarly ? kItems : 1];
+    if constexpr (kEarly) {
+        if (a.bias != nullptr) {
 #pragma unroll
-        for (int t = 0; t < kItems; ++t) bsv[t] = a.bias[sample_latent(item(t), a.samp_log2)];   // 4-byte aligned only
-    } else {
+            for (int t = 0; t < kItems; ++t) bsv[t] = a.bias[sample_latent(item(t), a.samp_log2)];   // 4-byte aligned only
+        } else {
 #pragma unroll
-        for (int t = 0; t < kItems; ++t) bsv[t] = 0.f;
+            for (int t = 0; t < kItems; ++t) bsv[t] = 0.f;
+        }
     }
     f32x4 v[kQuads];
     for (int sp0 = 0; sp0 < a.nsplit; sp0 += kSplitBatch) {
@@ -483,7 +489,8 @@ __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
     }
     if (a.bias != nullptr) {
 #pragma unroll
-        for (int t = 0; t < kItems; ++t) v[t >> 2][t & 3] += bsv[t];
+        for (int t = 0; t < kItems; ++t)
+            v[t >> 2][t & 3] += kEarly ? bsv[kEarly ? t : 0] : a.bias[sample_latent(item(t), a.samp_log2)];
     }
     uint64_t key[kItems];
     uint64_t m = 0;
