@@ -427,9 +427,9 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         // the head holds at most k keys (nsamp <= kSelCap): one segment per
         // merge thread, read in place, in passes of 30 keys where a segment
         // expects at most ~12 (k * F / nsamp keys per row over the
-        // workgroups), else of 62
+        // workgroups), of 46 up to ~24, else of 62
         const int64_t per_seg = p.sample ? cdiv(k * F / p.nsamp, p.nwg) : p.cap;
-        mg.spec = per_seg <= 12 ? 3 : 4;
+        mg.spec = per_seg <= 12 ? 3 : per_seg <= 24 ? 4 : 5;
     }
     mg.k = (int)k;
     mg.f_offset = (int32_t)f_offset;

@@ -969,7 +969,9 @@ hipError_t launch_merge(const MergeArgs& a, int64_t rows, hipStream_t st)
         launch(merge_kernel<32, 0>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     else if (a.spec == 3)   // segments expected to hold up to ~12 keys: 30 per pass
         launch(merge_seg_kernel<30, 16>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
-    else if (a.spec == 4)   // fuller segments: 62 per pass, so that one pass covers them
+    else if (a.spec == 4)   // segments expected to hold up to ~24 keys: 46 per pass
+        launch(merge_seg_kernel<46, 16>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+    else if (a.spec == 5)   // fuller segments: 62 per pass
         launch(merge_seg_kernel<62, 16>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     else
         launch(merge_kernel<16, 0>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
