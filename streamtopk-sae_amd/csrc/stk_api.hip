@@ -424,10 +424,10 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         if (e != hipSuccess) return hip_fail(e, "main_kernel launch");
         mg.list_keys = list_keys; mg.list_cnt = list_cnt; mg.list_cap = p.list_cap;
         mg.head_span = p.head_span; mg.nseg = p.nwg; mg.seg_cap = p.cap; mg.seg_cnt = seg_cnt;
-        // the head holds at most k keys (nsamp <= kSelCap): one segment per
-        // merge thread, read in place, in passes of 30 keys where a segment
+        // the head holds at most k keys (nsamp <= kSelCap): two merge threads
+        // per segment, read in place, in passes of 32 keys where a segment
         // expects at most ~12 (k * F / nsamp keys per row over the
-        // workgroups), of 46 up to ~24, else of 62
+        // workgroups), of 48 up to ~24, else of 64
         const int64_t per_seg = p.sample ? cdiv(k * F / p.nsamp, p.nwg) : p.cap;
         mg.spec = per_seg <= 12 ? 3 : per_seg <= 24 ? 4 : 5;
     }

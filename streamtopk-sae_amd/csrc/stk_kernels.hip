@@ -435,10 +435,10 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a)
 // real scores reach it, so it never exceeds the row's final k-th key); the
 // sampled keys that reach it -- the sample's top k -- are written to the
 // list, since main_kernel skips the sampled latents.
-template <int kItems>
-__global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
+template <int kItems, int NT>
+__global__ __launch_bounds__(NT) void thr_kernel(ThrArgs a)
 {
-    __shared__ SelShared S;
+    __shared__ SelSharedT<NT> S;
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
     if (row == 0 && tid == 0) *a.err = 0u;   // the first kernel that runs after it is read
@@ -446,15 +446,15 @@ __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
         if (tid == 0) { a.thr[row] = 0; a.list_cnt[row * kCntStride] = 0; }
         return;
     }
-    // item t of this thread is sampled latent 4 * tid + kThreads * 4 * (t / 4) + t % 4:
+    // item t of this thread is sampled latent 4 * tid + NT * 4 * (t / 4) + t % 4:
     // four consecutive sampled latents (one 16-byte load of P) per quad
     constexpr int kQuads = kItems / 4;
-    auto item = [&](int t) { return 4 * tid + kThreads * 4 * (t >> 2) + (t & 3); };
+    auto item = [&](int t) { return 4 * tid + NT * 4 * (t >> 2) + (t & 3); };
     const float* prow = a.P + row * a.p_row;
     const int64_t split_stride = a.p_split;
-    // With 16 items per thread the bias of the sampled latents goes out first
-    // (it does not depend on P) and the splits' partial sums four splits at a
-    // time with all their loads in flight; with 32 items (the larger sample),
+    // With up to 16 items per thread (both launches) the bias of the sampled
+    // latents goes out first (it does not depend on P) and the splits' partial
+    // sums four splits at a time with all their loads in flight; with more,
     // whose keys fill the registers, one split at a time and the bias last, as
     // more loads in flight would cost occupancy.  Either way the sums are added
     // in split order, then the bias.
@@ -518,7 +518,7 @@ __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
     const int n = S.cnt;   // >= k: at least k sampled keys reach T0
     uint64_t T = T0;
     uint64_t* out = a.list_keys + row * a.list_cap;
-    if (n <= kThreads) {
+    if (n <= NT) {
         // the sample's k largest keys by rank, counted (thread t ranks key
         // t): the key of rank k - 1 is the threshold
         if (tid < n) {
@@ -559,8 +559,8 @@ __global__ __launch_bounds__(kThreads) void thr_kernel(ThrArgs a)
 // per-thread maxima: k of the pass's keys reach it) and `run` (the k-th key of
 // the last compaction) go to S.buf; when it fills, it is compacted to its top
 // k, which raises `run`.  Every thread of the workgroup takes part.
-template <int N>
-__device__ __forceinline__ void merge_pass(SelShared& S, const uint64_t (&v)[N], int k, int tid, uint64_t& run)
+template <int N, int NT>
+__device__ __forceinline__ void merge_pass(SelSharedT<NT>& S, const uint64_t (&v)[N], int k, int tid, uint64_t& run)
 {
     static_assert(N <= 64, "pending mask");
     using Mask = std::conditional_t<(N > 32), uint64_t, uint32_t>;
@@ -612,25 +612,26 @@ __device__ __forceinline__ void merge_pass(SelShared& S, const uint64_t (&v)[N],
 // Whether the call's error word is set (a streaming kernel lost candidates);
 // if so, row `row` of the output is marked: indices -1, values NaN.  The word
 // is the same for every thread, so the whole workgroup returns together.
+template <int NT = kThreads>
 __device__ __forceinline__ bool merge_marked(const MergeArgs& a, int64_t row, int tid)
 {
     if (a.err == nullptr || *a.err == 0u) return false;
-    for (int r = tid; r < a.k; r += kThreads) {
+    for (int r = tid; r < a.k; r += NT) {
         a.V[row * a.k + r] = __builtin_nanf("");
         a.I[row * a.k + r] = -1;
     }
     return true;
 }
 
-template <int kPer, int kSpec>
-__global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
+template <int kPer, int kSpec, int NT>
+__global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a)
 {
-    __shared__ SelShared S;
+    __shared__ SelSharedT<NT> S;
     __shared__ int scnt[kMergeMaxSeg];
     __shared__ int spre[kMergeMaxSeg];   // inclusive prefix sums of scnt
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
-    if (merge_marked(a, row, tid)) return;
+    if (merge_marked<NT>(a, row, tid)) return;
     const int k = a.k;
     const int nseg = a.nseg;
     const int64_t hc = a.list_cnt[row * kCntStride];
@@ -638,10 +639,10 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
     uint64_t v[kPer];
 #pragma unroll
     for (int u = 0; u < kSpec; ++u) {
-        const int64_t i = tid + (int64_t)u * kThreads;
+        const int64_t i = tid + (int64_t)u * NT;
         v[u] = keys[i < a.list_cap ? i : a.list_cap - 1];
     }
-    for (int sg = tid; sg < nseg; sg += kThreads) scnt[sg] = a.seg_cnt[row * nseg + sg];
+    for (int sg = tid; sg < nseg; sg += NT) scnt[sg] = a.seg_cnt[row * nseg + sg];
     if (tid == 0) S.cnt = 0;
     __syncthreads();
     // Candidate i (0 <= i < n) is head key i for i < hc, else key i - hc of
@@ -668,14 +669,14 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
         top = 1 << (31 - __builtin_clz(nseg));
     }
     uint64_t run = 0;
-    for (int64_t c0 = 0; c0 < n; c0 += (int64_t)kPer * kThreads) {
+    for (int64_t c0 = 0; c0 < n; c0 += (int64_t)kPer * NT) {
         if (nseg > 0) {
             // segment of each segment candidate: the number of segments whose
             // inclusive prefix is <= its index (all items searched in step)
             int j[kPer], pos[kPer];
 #pragma unroll
             for (int u = 0; u < kPer; ++u) {
-                j[u] = (int)(c0 + tid + (int64_t)u * kThreads - hc);
+                j[u] = (int)(c0 + tid + (int64_t)u * NT - hc);
                 pos[u] = 0;
             }
             for (int st = top; st > 0; st >>= 1) {
@@ -687,7 +688,7 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
             }
 #pragma unroll
             for (int u = 0; u < kPer; ++u) {
-                const int64_t i = c0 + tid + (int64_t)u * kThreads;
+                const int64_t i = c0 + tid + (int64_t)u * NT;
                 if (i >= n) {
                     v[u] = 0ull;
                 } else if (i < hc) {
@@ -701,7 +702,7 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
         } else {
 #pragma unroll
             for (int u = 0; u < kPer; ++u) {
-                const int64_t i = c0 + tid + (int64_t)u * kThreads;
+                const int64_t i = c0 + tid + (int64_t)u * NT;
                 const bool ok = i < n;
                 if (u < kSpec && c0 == 0)
                     v[u] = ok ? v[u] : 0ull;
@@ -723,20 +724,27 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a)
 
 // Per row: top-k of main_kernel's list -- a head of at most kThreads keys,
 // then nseg segments of seg_cap slots, segment s holding seg_cnt[row * nseg +
-// s] keys.  Thread t reads head key t and the keys of segments t, t +
-// kThreads, ..., kPer consecutive keys per pass (16-byte loads): no search for
-// a key's segment, and every thread has its loads in flight at once.  The
-// head key and the first kEager keys of a segment (one 128-byte line) are
-// loaded without waiting for the counts and masked afterwards.  A pass filters
-// as merge_kernel's chunks.
-template <int kPer, int kEager>
-__global__ __launch_bounds__(kThreads) void merge_seg_kernel(MergeArgs a)
+// s] keys.  NT = SPLIT * kThreads threads; the SPLIT threads of slot t
+// (threads SPLIT * t ..) read segments t, t + kThreads, ..., the keys in
+// pairs dealt round-robin (pair j of a segment to thread j % SPLIT), kPer keys
+// per thread and pass (16-byte loads, adjacent threads on adjacent pairs):
+// no search for a key's segment, and every thread has its loads in flight at
+// once.  Thread t also reads head key t.  The head key and the first kEager
+// keys per thread of a segment (SPLIT * kEager keys) are loaded without
+// waiting for the counts and masked afterwards.  A pass filters as
+// merge_kernel's chunks.
+template <int kPer, int kEager, int NT>
+__global__ __launch_bounds__(NT) void merge_seg_kernel(MergeArgs a)
 {
     static_assert(kPer % 2 == 0 && kEager % 2 == 0 && kEager <= kPer, "pairs of keys");
-    __shared__ SelShared S;
+    static_assert(NT % kThreads == 0, "whole slots");
+    constexpr int SPLIT = NT / kThreads;
+    constexpr int kStep = SPLIT * kPer;   // keys of a segment per pass
+    __shared__ SelSharedT<NT> S;
     const int tid = threadIdx.x;
+    const int slot = tid / SPLIT, part = tid % SPLIT;
     const int64_t row = blockIdx.x;
-    if (merge_marked(a, row, tid)) return;
+    if (merge_marked<NT>(a, row, tid)) return;
     const int k = a.k;
     const int nseg = a.nseg;
     const int64_t hs = a.head_span;   // <= kThreads (host)
@@ -747,34 +755,37 @@ __global__ __launch_bounds__(kThreads) void merge_seg_kernel(MergeArgs a)
     if (tid == 0) S.cnt = 0;
     uint64_t run = 0;
     for (int s0 = 0; s0 < nseg || s0 == 0; s0 += kThreads) {
-        const int sg = s0 + tid;
+        const int sg = s0 + slot;
         const bool own = sg < nseg;
-        // segment starts are 16-byte aligned (head_span and seg_cap even)
-        const uint64_t* q = keys + hs + (int64_t)(own ? sg : 0) * a.seg_cap;
+        // segment starts are 16-byte aligned (head_span and seg_cap even);
+        // this thread's pair u / 2 of a pass starts at key base + SPLIT * u +
+        // 2 * part of the segment
+        const uint64_t* q = keys + hs + (int64_t)(own ? sg : 0) * a.seg_cap + 2 * part;
         u64x2 e[kEager / 2];
 #pragma unroll
         for (int u = 0; u < kEager; u += 2) {
             e[u / 2] = u64x2{0ull, 0ull};
-            if (own && u < a.seg_cap) e[u / 2] = *(const u64x2*)(q + u);
+            if (own && SPLIT * u + 2 * part < a.seg_cap) e[u / 2] = *(const u64x2*)(q + SPLIT * u);
         }
-        const int cnt = own ? a.seg_cnt[row * nseg + sg] : 0;
+        const int cnt = (own ? a.seg_cnt[row * nseg + sg] : 0) - 2 * part;
         if (s0 == 0 && tid >= hc) v[kPer] = 0ull;
-        for (int base = 0;; base += kPer) {
+        for (int base = 0;; base += kStep) {
 #pragma unroll
             for (int u = 0; u < kPer; u += 2) {
                 // a pair starting below the count lies inside the segment
-                // (cnt <= seg_cap, both even)
+                // (pair starts and seg_cap are even, the count <= seg_cap)
+                const int o = base + SPLIT * u;
                 u64x2 p = {0ull, 0ull};
                 if (u < kEager && base == 0)
                     p = e[u / 2];
-                else if (base + u < cnt)
-                    p = *(const u64x2*)(q + base + u);
-                v[u] = base + u < cnt ? p[0] : 0ull;
-                v[u + 1] = base + u + 1 < cnt ? p[1] : 0ull;
+                else if (o < cnt)
+                    p = *(const u64x2*)(q + o);
+                v[u] = o < cnt ? p[0] : 0ull;
+                v[u + 1] = o + 1 < cnt ? p[1] : 0ull;
             }
             merge_pass(S, v, k, tid, run);
             v[kPer] = 0ull;
-            if (!__syncthreads_or(cnt > base + kPer)) break;
+            if (!__syncthreads_or(cnt > base + kStep - 2 * part)) break;
         }
     }
     emit_topk(S, k, tid, [&](int r, uint64_t kk) {
@@ -937,11 +948,13 @@ hipError_t launch_sample(int dt, int NB, const SampleArgs& a, dim3 grid, hipStre
 hipError_t launch_thr(const ThrArgs& a, int64_t rows, hipStream_t st)
 {
     if (a.P != nullptr && a.nsamp == kSampleLarge) {
-        launch(thr_kernel<kSampleLarge / kThreads>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+        // the larger sample on 512 threads (16 keys each): 27.9 -> 25.6 us
+        // at B = 1024; the 4096-latent one gains nothing from it
+        launch(thr_kernel<kSampleLarge / (2 * kThreads), 2 * kThreads>, dim3((unsigned)rows), dim3(2 * kThreads), 0, st, a);
         return hipGetLastError();
     }
     if (a.P != nullptr && a.nsamp != kSampleTarget) return hipErrorInvalidValue;
-    launch(thr_kernel<kSampleTarget / kThreads>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+    launch(thr_kernel<kSampleTarget / kThreads, kThreads>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     return hipGetLastError();
 }
 
@@ -964,17 +977,17 @@ hipError_t launch_merge(const MergeArgs& a, int64_t rows, hipStream_t st)
     // otherwise 16 slots per thread, which also keeps the registers low enough
     // for four workgroups per CU when the rows are many (large batches)
     if (a.spec == 1)
-        launch(merge_kernel<32, 16>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+        launch(merge_kernel<32, 16, kThreads>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     else if (a.spec == 2)
-        launch(merge_kernel<32, 0>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
-    else if (a.spec == 3)   // segments expected to hold up to ~12 keys: 30 per pass
-        launch(merge_seg_kernel<30, 16>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
-    else if (a.spec == 4)   // segments expected to hold up to ~24 keys: 46 per pass
-        launch(merge_seg_kernel<46, 16>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
-    else if (a.spec == 5)   // fuller segments: 62 per pass
-        launch(merge_seg_kernel<62, 16>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+        launch(merge_kernel<32, 0, kThreads>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+    else if (a.spec == 3)   // segments expected to hold up to ~12 keys: 32 per pass
+        launch(merge_seg_kernel<16, 8, 2 * kThreads>, dim3((unsigned)rows), dim3(2 * kThreads), 0, st, a);
+    else if (a.spec == 4)   // segments expected to hold up to ~24 keys: 48 per pass
+        launch(merge_seg_kernel<24, 8, 2 * kThreads>, dim3((unsigned)rows), dim3(2 * kThreads), 0, st, a);
+    else if (a.spec == 5)   // fuller segments: 64 per pass
+        launch(merge_seg_kernel<32, 8, 2 * kThreads>, dim3((unsigned)rows), dim3(2 * kThreads), 0, st, a);
     else
-        launch(merge_kernel<16, 0>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+        launch(merge_kernel<16, 0, kThreads>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     return hipGetLastError();
 }
 

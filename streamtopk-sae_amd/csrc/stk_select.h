@@ -10,16 +10,20 @@ namespace stk {
 constexpr int kSelCap = 4096;   // keys held in LDS by one selection workgroup
 constexpr int kMaxK = 128;
 
-struct SelShared {
+// The LDS state of one selection workgroup of NT threads (NT / 64 waves).
+template <int NT>
+struct SelSharedT {
+    static constexpr int NW = NT / 64;
     uint64_t buf[kSelCap];
-    uint32_t hist[kWaves][256];
+    uint32_t hist[NW][256];
     uint64_t sel[kMaxK];
-    uint64_t tmax[kThreads];
-    uint64_t wthr[kWaves];
+    uint64_t tmax[NT];
+    uint64_t wthr[NW];
     uint64_t prefix, mask, thr;
     uint32_t remaining;
     int cnt, sel_cnt, done;
 };
+using SelShared = SelSharedT<kThreads>;
 
 // Slots for c >= 0 items of each lane from the LDS counter *ctr, with one
 // atomic per wave (same-address LDS atomics serialise lane by lane): returns
@@ -52,15 +56,17 @@ __device__ inline int wave_reserve1(int* ctr, bool f)
 
 // Every thread passes the largest key it holds (0 if none).  Returns a key T
 // such that at least k keys are >= T, or 1 (accept every real key) when a
-// wave holds too few keys.  k is split over the waves (k_w = k / kWaves, the
-// first k % kWaves waves one more); wave w's bound is the k_w-th largest of
+// wave holds too few keys.  k is split over the NW waves (k_w = k / NW, the
+// first k % NW waves one more); wave w's bound is the k_w-th largest of
 // its 64 maxima, which are themselves keys, and T is the smallest bound over
 // the waves with k_w > 0: at least sum k_w = k keys reach T.  Ranking within
-// a wave costs a quarter of ranking all the workgroup's maxima.
-__device__ inline uint64_t kth_of_maxima(SelShared& S, uint64_t m, int k, int tid)
+// a wave costs 1 / NW of ranking all the workgroup's maxima.
+template <int NT>
+__device__ inline uint64_t kth_of_maxima(SelSharedT<NT>& S, uint64_t m, int k, int tid)
 {
+    constexpr int NW = NT / 64;
     const int lane = tid & 63, wave = tid >> 6;
-    const int kw = k / kWaves + (wave < k % kWaves ? 1 : 0);
+    const int kw = k / NW + (wave < k % NW ? 1 : 0);
     S.tmax[tid] = m;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -91,22 +97,24 @@ __device__ inline uint64_t kth_of_maxima(SelShared& S, uint64_t m, int k, int ti
     __syncthreads();
     uint64_t T = S.wthr[0];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) T = S.wthr[w] < T ? S.wthr[w] : T;
+    for (int w = 1; w < NW; ++w) T = S.wthr[w] < T ? S.wthr[w] : T;
     return T;
 }
 
 // Finds the digit prefix of the k-th largest key among buf[0..n): afterwards
 // exactly k keys satisfy (key & S.mask) >= S.prefix.  Requires n >= k >= 1.
-__device__ inline void radix_kth(SelShared& S, int n, int k, int tid)
+template <int NT>
+__device__ inline void radix_kth(SelSharedT<NT>& S, int n, int k, int tid)
 {
+    constexpr int NW = NT / 64;
     const int lane = tid & 63, wave = tid >> 6;
     if (tid == 0) { S.prefix = 0; S.mask = 0; S.remaining = (uint32_t)k; S.done = 0; }
     __syncthreads();
     for (int shift = 56; shift >= 0; shift -= 8) {
-        for (int i = tid; i < kWaves * 256; i += kThreads) (&S.hist[0][0])[i] = 0;
+        for (int i = tid; i < NW * 256; i += NT) (&S.hist[0][0])[i] = 0;
         __syncthreads();
         const uint64_t prefix = S.prefix, mask = S.mask;
-        for (int i = tid; i < n; i += kThreads) {
+        for (int i = tid; i < n; i += NT) {
             const uint64_t key = S.buf[i];
             if ((key & mask) == prefix) atomicAdd(&S.hist[wave][(key >> shift) & 255u], 1u);
         }
@@ -114,9 +122,11 @@ __device__ inline void radix_kth(SelShared& S, int n, int k, int tid)
         if (wave == 0) {
             uint32_t c[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                c[e] = S.hist[0][4 * lane + e] + S.hist[1][4 * lane + e] + S.hist[2][4 * lane + e] +
-                       S.hist[3][4 * lane + e];
+            for (int e = 0; e < 4; ++e) {
+                c[e] = S.hist[0][4 * lane + e];
+#pragma unroll
+                for (int w = 1; w < NW; ++w) c[e] += S.hist[w][4 * lane + e];
+            }
             const uint32_t lsum = c[0] + c[1] + c[2] + c[3];
             uint32_t suf = lsum;   // inclusive suffix sum over lanes
 #pragma unroll
@@ -150,13 +160,14 @@ __device__ inline void radix_kth(SelShared& S, int n, int k, int tid)
 
 // Keeps the k largest of buf[0..n) in buf[0..k) (unsorted); S.thr becomes the
 // smallest kept key.  Requires n > k.
-__device__ inline void select_compact(SelShared& S, int n, int k, int tid)
+template <int NT>
+__device__ inline void select_compact(SelSharedT<NT>& S, int n, int k, int tid)
 {
     radix_kth(S, n, k, tid);
     const uint64_t prefix = S.prefix, mask = S.mask;
     if (tid == 0) S.sel_cnt = 0;
     __syncthreads();
-    for (int i0 = 0; i0 < n; i0 += kThreads) {
+    for (int i0 = 0; i0 < n; i0 += NT) {
         const int i = i0 + tid;
         const uint64_t key = i < n ? S.buf[i] : 0ull;
         const bool f = i < n && (key & mask) >= prefix;
@@ -187,8 +198,8 @@ __device__ inline void select_compact(SelShared& S, int n, int k, int tid)
 // which keeps the ranks a permutation when a caller's keys repeat (shard
 // results merged by stk_topk_merge).  Every thread reads the same LDS words
 // (broadcast), 16 keys per round.
-template <bool kTies>
-__device__ inline int rank_desc(const SelShared& S, int n, uint64_t key, int pos)
+template <bool kTies, int NT>
+__device__ inline int rank_desc(const SelSharedT<NT>& S, int n, uint64_t key, int pos)
 {
     int r = 0;
     int i = 0;
@@ -211,16 +222,16 @@ __device__ inline int rank_desc(const SelShared& S, int n, uint64_t key, int pos
 }
 
 // Reduces buf[0..cnt) to its top k and calls emit(rank, key) for rank < k,
-// rank 0 being the largest.  Up to kThreads keys are ranked directly by
-// counting (thread t ranks key t), more are first reduced to the k largest by
-// radix selection.  Returns the number of keys emitted.
-template <bool kTies = false, class Emit>
-__device__ inline int emit_topk(SelShared& S, int k, int tid, Emit emit)
+// rank 0 being the largest.  Up to NT keys are ranked directly by counting
+// (thread t ranks key t), more are first reduced to the k largest by radix
+// selection.  Returns the number of keys emitted.
+template <bool kTies = false, int NT, class Emit>
+__device__ inline int emit_topk(SelSharedT<NT>& S, int k, int tid, Emit emit)
 {
     __syncthreads();
     int n = S.cnt < kSelCap ? S.cnt : kSelCap;
-    if (n > kThreads) {
-        select_compact(S, n, k, tid);   // k <= kMaxK <= kThreads keys remain
+    if (n > NT) {
+        select_compact(S, n, k, tid);   // k <= kMaxK <= NT keys remain
         n = k;
     }
     if (tid < n) {
