@@ -175,7 +175,19 @@ __device__ __forceinline__ void sort_segment(const GroupArgs& a, const uint32_t*
     // c < 128: only the top c are selected and ordered (entries c ..
     // 127 end up holding copies); c = 128: the full sort
     bitonic_topc<C>(v, l);
+    // Every LDS read of the checks below is issued before any is waited for:
+    // the staged words of this lane's entries (a position always lies inside
+    // the row), the entry after this lane's last, and for c < 128 the row's
+    // words again (rather than held through the network).
+    uint32_t word[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) word[j] = src[127u - (v[j] & 0x7Fu)];
     const uint32_t nx = __shfl_down(v[0], 1, 16);   // entry 8l + 8
+    u32x4 r0 = {0u, 0u, 0u, 0u}, r1 = {0u, 0u, 0u, 0u};
+    if constexpr (C < 128) {
+        r0 = *(const u32x4*)(src + 8 * l);
+        r1 = *(const u32x4*)(src + 8 * l + 4);
+    }
     bool tie = false;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -185,18 +197,27 @@ __device__ __forceinline__ void sort_segment(const GroupArgs& a, const uint32_t*
     if constexpr (C < 128) {
         // the (c+1)-th is not at hand: a real entry outside the top c
         // whose truncated word equals the c-th's shows as more than c
-        // real entries at or above that word
-        const uint32_t tc = __shfl(v[7], c / 8 - 1, 16) >> 7;   // entry c - 1
+        // real entries at or above that word.  Entry c - 1 is register 7
+        // of lane c/8 - 1 of this 16-lane row (read lane by lane: every
+        // lane of the wave is active), the count is summed over the row
+        // by rotations
+        const int rq = (int)(__lane_id() >> 4);
+        const uint32_t e0 = __builtin_amdgcn_readlane(v[7], c / 8 - 1);
+        const uint32_t e1 = __builtin_amdgcn_readlane(v[7], 16 + c / 8 - 1);
+        const uint32_t e2 = __builtin_amdgcn_readlane(v[7], 32 + c / 8 - 1);
+        const uint32_t e3 = __builtin_amdgcn_readlane(v[7], 48 + c / 8 - 1);
+        const uint32_t tc = (rq == 0 ? e0 : rq == 1 ? e1 : rq == 2 ? e2 : e3) >> 7;
         int above = 0;
-        // the words again from LDS, rather than held through the network
-        const u32x4 r0 = *(const u32x4*)(src + 8 * l), r1 = *(const u32x4*)(src + 8 * l + 4);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const uint32_t ov = j < 4 ? r0[j] : r1[j - 4];
             above += (ov != 0u && (ov >> 7) >= tc) ? 1 : 0;
         }
-#pragma unroll
-        for (int m = 1; m < 16; m <<= 1) above += __shfl_xor(above, m, 16);
+        // row_ror:8, 4, 2, 1: every lane ends with the row's sum
+        above += __builtin_amdgcn_mov_dpp(above, 0x128, 0xF, 0xF, false);
+        above += __builtin_amdgcn_mov_dpp(above, 0x124, 0xF, 0xF, false);
+        above += __builtin_amdgcn_mov_dpp(above, 0x122, 0xF, 0xF, false);
+        above += __builtin_amdgcn_mov_dpp(above, 0x121, 0xF, 0xF, false);
         tie |= tc != 0u && above != c;
     }
     float val[8];
@@ -207,16 +228,16 @@ __device__ __forceinline__ void sort_segment(const GroupArgs& a, const uint32_t*
         for (int j = 0; j < 8; ++j) {
             const uint32_t pos = 127u - (v[j] & 0x7Fu);
             const bool real = (v[j] >> 7) != 0;
-            val[j] = real ? key_value((uint64_t)src[pos] << 32) : -3.402823466e+38f;
+            val[j] = real ? key_value((uint64_t)word[j] << 32) : -3.402823466e+38f;
             idx[j] = real ? fg + pos : 0xFFFFFFFFu;
         }
     } else {
         // full keys for this wave's four segments
         uint64_t u[8];
-        const u32x4 r0 = *(const u32x4*)(src + 8 * l), r1 = *(const u32x4*)(src + 8 * l + 4);
+        const u32x4 q0 = *(const u32x4*)(src + 8 * l), q1 = *(const u32x4*)(src + 8 * l + 4);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const uint32_t ov = j < 4 ? r0[j] : r1[j - 4];
+            const uint32_t ov = j < 4 ? q0[j] : q1[j - 4];
             u[j] = ov ? (((uint64_t)ov << 32) | (0xFFFFFFFFu - (fg + 8 * l + j))) : 0ull;
         }
         bitonic_sort128(u, l);

@@ -191,3 +191,51 @@ def test_candidates_full_row_blocks(cuda_dev, dtype, B, d, F):
     rows = slice(0, 16)
     S = oracle.scores_f64(_np(X[rows]), _np(W), _np(b))
     check_against_scores(V[rows].cpu().numpy(), I[rows].cpu().numpy(), S, k, tol, "full row blocks")
+
+
+def _tie_heavy_inputs(B, d, F, seed):
+    """fp32 inputs whose scores are chosen exactly: X[r] is the unit vector
+    e_(r % d) and b_enc is 0, so score[r, f] = W[f, r % d] with no rounding.
+    Each (group, column) gets one of five patterns: 128 distinct values inside
+    one 2^-16 relative bucket (every ordered word equal once its low 7 bits
+    are dropped), a few such buckets, exact duplicates, negatives inside one
+    bucket, and plain Gaussian values."""
+    rng = np.random.default_rng(seed)
+    X = np.zeros((B, d), dtype=np.float32)
+    X[np.arange(B), np.arange(B) % d] = 1.0
+    W = np.empty((F, d), dtype=np.float32)
+    ulp = np.float32(2.0 ** -23)
+    for g0 in range(0, F, 128):
+        n = min(128, F - g0)
+        for j in range(d):
+            kind = rng.integers(0, 5)
+            if kind == 0:
+                v = 1 + rng.permutation(128)[:n].astype(np.float32) * ulp
+            elif kind == 1:
+                v = 1 + (rng.integers(0, 3, n) * 128 + rng.permutation(128)[:n]).astype(np.float32) * ulp
+            elif kind == 2:
+                v = 1 + rng.integers(0, 24, n).astype(np.float32) * ulp * 128
+            elif kind == 3:
+                v = -(1 + rng.permutation(128)[:n].astype(np.float32) * ulp)
+            else:
+                v = rng.standard_normal(n).astype(np.float32)
+            W[g0:g0 + n, j] = v
+    return X, W, np.zeros(F, dtype=np.float32)
+
+
+@pytest.mark.parametrize("c", [16, 32, 64, 128])
+def test_approx_candidates_truncated_ties(cuda_dev, c):
+    """Per-group selection where the scores tie once truncated to 25 bits
+    (and some tie exactly): the candidates must equal the oracle's bit for bit
+    (values identify the latents here), and the final top-k exactly."""
+    print(f"case approx candidates truncated ties c={c}", flush=True)
+    B, d, F = 40, 32, 1280 + 77
+    k = min(16, c)
+    Xn, Wn, bn = _tie_heavy_inputs(B, d, F, seed=40 + c)
+    X, W, b = (torch.from_numpy(a).to(cuda_dev) for a in (Xn, Wn, bn))
+    nt = (F + 127) // 128
+    cb = torch.empty((B, nt, c), dtype=torch.float32, device=cuda_dev)
+    V, I = topk_sae_cuda_approx(X, W, b, k, c, candidate_buffer=cb)
+    Vo, Io, cvo, cio = oracle.approx(Xn, Wn, bn, k, c, with_candidates=True)
+    assert np.array_equal(cb.cpu().numpy(), cvo)
+    assert np.array_equal(V.cpu().numpy(), Vo) and np.array_equal(I.cpu().numpy(), Io)
