@@ -2,9 +2,9 @@
 checked against the oracle's float64 scores on a row subset:
 
 * B around one 32-row block, four blocks (128) and the large-batch kernel's
-  threshold (512);
-* F around the 256-latent tile, the 128-latent group and the sampling
-  threshold (16384);
+  threshold (512), and 1024;
+* F around the 256-latent tile, the 128-latent group, the sampling
+  threshold (16384) and the larger sample's (131072);
 * d ragged (a partial last 128-byte step) and a multiple of it;
 * k from 1 to 128, every dtype, the exact op and the approximate op (with and
   without a candidate buffer).
@@ -28,12 +28,12 @@ _DT = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}
 
 def _cases():
     rng = np.random.default_rng(2026)
-    Bs = [1, 31, 33, 96, 97, 127, 128, 129, 255, 511, 512, 520]
-    Fs = [100, 255, 257, 1000, 4096, 16383, 16384, 16385, 40000, 70001]
+    Bs = [1, 31, 33, 96, 97, 127, 128, 129, 255, 511, 512, 520, 1024]
+    Fs = [100, 255, 257, 1000, 4096, 16383, 16384, 16385, 40000, 70001, 131073]
     ds = [8, 64, 72, 200, 256, 768, 1000]
     ks = [1, 2, 4, 8, 16, 32, 64, 128]
     out = []
-    for i in range(28):
+    for i in range(84):
         B = int(rng.choice(Bs))
         F = int(rng.choice(Fs))
         d = int(rng.choice(ds))
