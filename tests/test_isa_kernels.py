@@ -1,0 +1,70 @@
+"""Code-generation checks of the exact path's kernels, without a GPU: the
+gfx950 assembly of csrc/stk_kernels.hip, compiled here with the build's flags.
+
+No kernel may use scratch memory (a register spill or an indexed register
+array), including the 512-thread selection kernels (the merge's two threads
+per segment, the large sample's threshold), whose thread count halves the
+registers a lane may hold.  main_kernel (8 waves, two per SIMD) must stay
+within 256 VGPRs per lane.
+"""
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+SRC = os.path.join(ROOT, "streamtopk-sae_amd", "csrc", "stk_kernels.hip")
+HIPCC = "/opt/rocm/bin/hipcc"
+
+pytestmark = pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
+
+
+@pytest.fixture(scope="module")
+def asm(tmp_path_factory):
+    out = tmp_path_factory.mktemp("isa") / "stk_kernels.s"
+    cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17",
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+           "--cuda-device-only", "-S", SRC, "-o", str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0, res.stderr[-2000:]
+    return out.read_text()
+
+
+def _kernels(asm):
+    return re.findall(r"^\s+\.name:\s+(_ZN3stk\w+)\s*$", asm, re.M)
+
+
+def _meta(asm, name):
+    i = asm.index(".name:           " + name)
+    start = asm.rindex(".agpr_count:", 0, i)
+    end = asm.find(".agpr_count:", i)
+    return asm[start:end if end > 0 else len(asm)]
+
+
+def test_every_kernel_without_scratch(asm):
+    names = _kernels(asm)
+    # main, sample, thr (two sizes), merge (dense and segmented), pack, probe
+    for part in ("main_kernel", "sample_kernel", "thr_kernel", "merge_kernel", "merge_seg_kernel",
+                 "pack_kernel", "read_probe_kernel"):
+        assert any(part in n for n in names), part
+    for n in names:
+        meta = _meta(asm, n)
+        assert re.search(r"\.private_segment_fixed_size:\s+0\b", meta), n
+        assert re.search(r"\.vgpr_spill_count:\s+0\b", meta), n
+        body = asm[asm.index(n + ":"):asm.index(".Lfunc_end", asm.index(n + ":"))]
+        assert not re.search(r"\bscratch_(load|store)", body), n
+
+
+def test_selection_kernels_at_512_threads(asm):
+    names = _kernels(asm)
+    wide = [n for n in names if ("merge_seg_kernel" in n or "thr_kernel" in n) and "Li512E" in n]
+    # the three merge widths and the large sample's threshold
+    assert len(wide) == 4, wide
+
+
+def test_main_kernel_registers(asm):
+    for n in _kernels(asm):
+        if "main_kernel" in n:
+            vgpr = int(re.search(r"\.vgpr_count:\s+(\d+)", _meta(asm, n)).group(1))
+            assert vgpr <= 256, (n, vgpr)
