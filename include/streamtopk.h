@@ -18,6 +18,11 @@
  *   - Device entry points run asynchronously on `stream` (a hipStream_t, NULL
  *     for the legacy default stream) on the current HIP device; all pointers
  *     must be device pointers on that device, 16-byte aligned.
+ *   - A workspace must be zero-filled before its first use (hipMemset once,
+ *     when it is allocated); every call leaves it valid for the next call of
+ *     any shape.  Calls that overlap in time must not share a workspace.
+ *     (The exact path's workgroups exchange per-row thresholds through words
+ *     tagged with the call's number; zero is never a call's tag.)
  */
 #ifndef STREAMTOPK_H
 #define STREAMTOPK_H

@@ -2,6 +2,11 @@
 // reference's error wording, launch planning for the current device, and the
 // kernel sequence of each entry point.  No device memory is allocated here:
 // every temporary lives in the caller's workspace.
+#include <unistd.h>
+
+#include <atomic>
+#include <chrono>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -155,8 +160,29 @@ static int ilog2_floor(int64_t x) { int l = 0; while ((x >> (l + 1)) > 0) ++l; r
 // ---------------------------------------------------------------------------
 // Exact-path plan
 // ---------------------------------------------------------------------------
+// The tag of one call's kernels (MainArgs::nonce): distinct for every call
+// of the process, and its low 32 bits (the exchange's word tag) are never 0
+// and differ between consecutive calls.  The sequence starts at a value drawn
+// from the clock, the process id and an address.
+static uint64_t next_nonce()
+{
+    static std::atomic<uint64_t> ctr{[] {
+        uint64_t z = (uint64_t)std::chrono::steady_clock::now().time_since_epoch().count();
+        z ^= (uint64_t)getpid() << 32;
+        z ^= (uint64_t)(uintptr_t)&g_err;
+        // splitmix64 finaliser
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        return z ^ (z >> 31);
+    }()};
+    uint64_t n;
+    do { n = ctr.fetch_add(1, std::memory_order_relaxed) + 1; } while ((uint32_t)n == 0);
+    return n;
+}
+
 struct ExactPlan {
     bool large;                  // mainl_kernel (B >= kLargeMinB) instead of main_kernel
+    bool xch;                    // main_kernel exchanges thresholds after its first tile (no sample pass)
     int NB, cap, lq;             // lq: main_kernel's LDS queue keys per row
     int64_t nbc, num_tiles, tpw;
     int nwg;                     // main_kernel: W ranges; mainl_kernel: nr (grid = nbc * nr)
@@ -165,7 +191,8 @@ struct ExactPlan {
     int ksplit;                  // d ranges (splits) of the sample pass
     int snb;                     // sample_kernel: 32-row tiles per workgroup
     int64_t list_cap, head_span;
-    size_t off_thr, off_list, off_lcnt, off_seg, total;
+    int64_t expect_seg;          // keys a segment is expected to receive (merge pass width)
+    size_t off_thr, off_list, off_lcnt, off_seg, off_xmax, off_xthr, total;
 };
 
 static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int dtype, int ncu)
@@ -197,7 +224,12 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
         p.nwg = (int)cdiv(p.num_tiles, p.tpw);
     }
 
-    p.sample = F >= kSampleMinF;
+    // Without a large batch, the first tile of every workgroup seeds the
+    // thresholds (each row's k-th largest of the workgroups' maxima) when
+    // there are enough workgroups for a k-th; otherwise a sample pass does.
+    // (STK_TEST_NO_XCH, a test hook read at each call, selects the sample pass)
+    p.xch = !p.large && p.nwg >= kXchMinWg && p.nwg >= k && p.nwg <= 256 && !std::getenv("STK_TEST_NO_XCH");
+    p.sample = F >= kSampleMinF && !p.xch;
     p.samp_log2 = 0;
     p.nsamp = 0;
     if (p.sample) {
@@ -236,15 +268,30 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
         // k * F / nsamp per row, spread over the workgroups), up to what fits
         // next to its rings; without a sample every score passes at first and
         // the queue takes all the room there is.
+        // With the exchange, a row's threshold is the k-th largest of nwg
+        // maxima over 256 latents each: a latent passes with probability
+        // about -ln(1 - k / nwg) / 256, so a workgroup expects
+        // -ln(1 - k / nwg) * tpw survivors per row.
         const int lq_max = main_lds_queue(p.NB, (int)k);
         int lq = lq_max;
-        if (p.sample) {
-            const int64_t expect = cdiv(k * F / p.nsamp, p.nwg);
+        p.expect_seg = p.cap;
+        if (p.sample || p.xch) {
+            int64_t expect;
+            if (p.xch) {
+                const double q = std::fmin((double)k / (double)p.nwg, 0.9);
+                expect = (int64_t)std::ceil(-std::log1p(-q) * (double)p.tpw);
+            } else {
+                expect = cdiv(k * F / p.nsamp, p.nwg);
+            }
+            p.expect_seg = expect;
             const int64_t want = (2 * expect + 8 + 1) & ~(int64_t)1;
             if (want < lq) lq = (int)want;
         }
         p.lq = lq;
         p.cap = (int)((k + p.lq + 1) & ~(int64_t)1);
+        if (!p.sample && !p.xch) p.expect_seg = p.cap;
+    } else {
+        p.expect_seg = p.cap;
     }
     // Each row's list: a head (the sample's top k; with a sample larger than
     // the selection buffer, every sampled key that reaches its first bound),
@@ -270,6 +317,14 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
     off = align256(off + (size_t)B * p.nwg * 4);
     p.off_list = off;
     off = align256(off + (size_t)B * p.list_cap * 8);
+    p.off_xmax = p.off_xthr = off;
+    if (p.xch) {
+        const size_t bt = 32 * (size_t)p.NB;
+        p.off_xmax = off;
+        off = align256(off + (size_t)p.nbc * p.nwg * bt * 8);
+        p.off_xthr = off;
+        off = align256(off + (size_t)p.nbc * bt * 8);
+    }
     p.total = off;
     return p;
 }
@@ -329,10 +384,15 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     uint64_t* list_keys = (uint64_t*)(ws + p.off_list);
     int32_t* list_cnt = (int32_t*)(ws + p.off_lcnt);
     int32_t* seg_cnt = (int32_t*)(ws + p.off_seg);
-    uint32_t* err = (uint32_t*)(list_cnt + B * kCntStride);
-    // STK_TEST_MAX_ROUNDS: the test hook that lowers the retry bounds
+    uint64_t* err = (uint64_t*)(list_cnt + B * kCntStride);
+    const uint64_t nonce = next_nonce();
+    // STK_TEST_MAX_ROUNDS: the test hook that lowers the retry bounds;
+    // STK_TEST_XCH_WAIT: the exchange's wait in ticks (0: every wait runs out
+    // at once, the path of workgroups that were never resident)
     int max_rounds = -1;
     if (const char* env = std::getenv("STK_TEST_MAX_ROUNDS")) max_rounds = std::atoi(env);
+    int64_t xwait = kXchWaitTicks;
+    if (const char* env = std::getenv("STK_TEST_XCH_WAIT")) xwait = std::atoll(env);
     // the sample's partial sums: in each row's segment area, split after split
     float* P = p.sample ? (float*)(list_keys + p.head_span) : nullptr;
     const int64_t p_row = 2 * p.list_cap, p_split = p.nsamp;
@@ -368,19 +428,20 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         prof_end(pi, st);
         if (e != hipSuccess) return hip_fail(e, "sample_kernel launch");
     }
-    ThrArgs ta;
-    ta.P = P;
-    ta.p_row = p_row;
-    ta.p_split = p_split;
-    ta.nsplit = p.ksplit;
-    ta.bias = b;
-    ta.samp_log2 = p.samp_log2; ta.nsamp = p.nsamp; ta.k = (int)k;
-    ta.thr = thr; ta.list_keys = list_keys; ta.list_cnt = list_cnt; ta.list_cap = p.list_cap;
-    ta.err = err;
-    int pt = prof_begin("thr_kernel", st);
-    e = launch_thr(ta, B, st);
-    prof_end(pt, st);
-    if (e != hipSuccess) return hip_fail(e, "thr_kernel launch");
+    if (!p.xch) {
+        ThrArgs ta;
+        ta.P = P;
+        ta.p_row = p_row;
+        ta.p_split = p_split;
+        ta.nsplit = p.ksplit;
+        ta.bias = b;
+        ta.samp_log2 = p.samp_log2; ta.nsamp = p.nsamp; ta.k = (int)k;
+        ta.thr = thr; ta.list_keys = list_keys; ta.list_cnt = list_cnt; ta.list_cap = p.list_cap;
+        int pt = prof_begin("thr_kernel", st);
+        e = launch_thr(ta, B, st);
+        prof_end(pt, st);
+        if (e != hipSuccess) return hip_fail(e, "thr_kernel launch");
+    }
     MergeArgs mg;
     if (p.large) {
         MainLArgs ml;
@@ -397,6 +458,7 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         ml.seg_cnt = seg_cnt;
         ml.max_rounds = max_rounds >= 0 ? max_rounds : kMainLMaxRounds;
         ml.err = err;
+        ml.nonce = nonce;
         int pm = prof_begin("main_kernel", st);
         e = launch_mainl(dt, ml, (int)(p.nbc * p.nwg), st);
         prof_end(pm, st);
@@ -406,10 +468,11 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         mg.spec = 0;
     } else {
         MainArgs ma;
+        std::memset(&ma, 0, sizeof ma);
         ma.X = X; ma.W = W; ma.bias = b; ma.B = B; ma.d = d; ma.F = F;
         ma.k = (int)k; ma.cap = p.cap;
         ma.num_tiles = p.num_tiles; ma.tiles_per_wg = p.tpw;
-        ma.thr0 = thr;
+        ma.thr0 = p.xch ? nullptr : thr;
         ma.sampled = p.sample ? 1 : 0;
         ma.samp_log2 = p.samp_log2;
         ma.samp_blocks = p.nsamp / kSampleBlock;
@@ -418,22 +481,27 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         ma.lq = p.lq;
         ma.max_rounds = max_rounds >= 0 ? max_rounds : kMainMaxRounds;
         ma.err = err;
+        ma.nonce = nonce;
+        ma.xch = p.xch ? 1 : 0;
+        ma.xmax = (uint64_t*)(ws + p.off_xmax);
+        ma.xthr = (uint64_t*)(ws + p.off_xthr);
+        ma.xwait = xwait;
         int pm = prof_begin("main_kernel", st);
         e = launch_main(dt, p.NB, ma, dim3((unsigned)p.nwg, (unsigned)p.nbc), st);
         prof_end(pm, st);
         if (e != hipSuccess) return hip_fail(e, "main_kernel launch");
         mg.list_keys = list_keys; mg.list_cnt = list_cnt; mg.list_cap = p.list_cap;
         mg.head_span = p.head_span; mg.nseg = p.nwg; mg.seg_cap = p.cap; mg.seg_cnt = seg_cnt;
-        // the head holds at most k keys (nsamp <= kSelCap): two merge threads
-        // per segment, read in place, in passes of 32 keys where a segment
-        // expects at most ~12 (k * F / nsamp keys per row over the
-        // workgroups), of 48 up to ~24, else of 64
-        const int64_t per_seg = p.sample ? cdiv(k * F / p.nsamp, p.nwg) : p.cap;
+        // the head holds at most k keys (nsamp <= kSelCap) or none: two
+        // merge threads per segment, read in place, in passes of 32 keys
+        // where a segment expects at most ~12, of 48 up to ~24, else of 64
+        const int64_t per_seg = p.expect_seg;
         mg.spec = per_seg <= 12 ? 3 : per_seg <= 24 ? 4 : 5;
     }
     mg.k = (int)k;
     mg.f_offset = (int32_t)f_offset;
     mg.err = err;
+    mg.nonce = nonce;
     mg.ties = 0;   // one encode's keys are distinct
     mg.V = V; mg.I = I;
     const int pg = prof_begin("merge_kernel", st);
@@ -492,8 +560,10 @@ static int validate_approx(int64_t B, int64_t d, int64_t F, int64_t k, int64_t c
 // hipGetSymbolAddress, resolved once per device with that device current,
 // and only that address is handed to kernels.  Nothing in it needs to start
 // at zero: every count and key a kernel reads is written earlier in the same
-// call (thr_kernel writes each row's threshold and head count, main_kernel
-// every segment count).
+// call (thr_kernel or the exchange each row's threshold, thr_kernel the head
+// counts, main_kernel every segment count), and the words compared with the
+// call's nonce (the exchange's flags, the error word) never hold it before
+// the call writes them.
 __attribute__((used)) static __device__ __align__(256) unsigned char scratch[STK_NOALLOC_SCRATCH_BYTES];
 
 static std::mutex g_scratch_mu;

@@ -302,7 +302,9 @@ __global__ __launch_bounds__(kMainThreads, 1) void group_kernel(GroupArgs a)
     ts.init_x((const unsigned char*)a.X, B, b0, a.d);
 
     f32x16 acc[NB];
-    ts.run(acc, smem, bias_lds, [&](int t, f32x16 (&ac)[NB], const float (&bias_r)[16]) {
+    // the accumulators start at the bias (as in main_kernel, so the two
+    // kernels' scores are bit-identical): ac holds the scores at the epilogue
+    ts.template run<true>(acc, smem, bias_lds, [&](int t, f32x16 (&ac)[NB], const float (&)[16]) {
         const int64_t tile = ts.tile_begin + t;
         const int64_t f0 = tile * kGroupTile;
         // accumulator register r of this lane: row 32n + jl, latent lt0 + 8*(r/4) + r%4
@@ -316,7 +318,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void group_kernel(GroupArgs a)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int r = 4 * q + i;
-                    o[i] = (f0 + lt0 + 8 * q + i < F) ? ordered_u32(ac[n][r] + bias_r[r]) : 0u;
+                    o[i] = (f0 + lt0 + 8 * q + i < F) ? ordered_u32(ac[n][r]) : 0u;
                 }
                 *(u32x4*)(ordv + jl * kOrdStride + lt0 + 8 * q) = o;
             }

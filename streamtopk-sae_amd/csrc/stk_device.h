@@ -234,7 +234,7 @@ __device__ __forceinline__ uint64_t compact_row(uint64_t* q, int n, uint64_t* sc
 // produce are never selected).
 //
 // run() calls epi(t, acc, bias) after the last d-step of tile t and then
-// clears acc and waits for every outstanding memory operation: the epilogue
+// resets acc and waits for every outstanding memory operation: the epilogue
 // may issue a data-dependent number of global stores, which the compiler
 // cannot count, and the wait restores its exact counts for the d-step loop
 // (the prefetched loads it includes have had the whole epilogue to land).
@@ -244,6 +244,10 @@ __device__ __forceinline__ uint64_t compact_row(uint64_t* q, int n, uint64_t* sc
 // writer runs after the epilogue, so an epilogue that uses it must end with a
 // workgroup barrier.  The bias of tile t comes from LDS: wave 0 loads the next
 // tile's bias inside the d-step loop and stores it within the same iteration.
+// With kBiasInit the accumulators of each tile start at the bias of their
+// latents (so acc holds the scores, bias included, when epi runs: the MFMAs
+// add the products onto it); otherwise they start at zero and epi receives
+// the bias to add.
 // ---------------------------------------------------------------------------
 template <int DT, int NB, int WAVES>
 struct TileStream {
@@ -401,7 +405,24 @@ struct TileStream {
         }
     }
 
-    template <class Epi>
+    __device__ __forceinline__ void acc_reset(f32x16 (&acc)[NB], const float* bias_buf, bool from_bias) const
+    {
+        if (from_bias) {
+            float bv[16];
+            bias_read(bv, bias_buf);
+#pragma unroll
+            for (int n = 0; n < NB; ++n)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[n][r] = bv[r];
+        } else {
+#pragma unroll
+            for (int n = 0; n < NB; ++n)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[n][r] = 0.f;
+        }
+    }
+
+    template <bool kBiasInit, class Epi>
     __device__ __forceinline__ void run(f32x16 (&acc)[NB], unsigned char* ring, float* bias_lds, Epi epi)
     {
         if (ntiles <= 0) return;
@@ -423,11 +444,8 @@ struct TileStream {
         issue(x1, w1);
         store(x0, w0, xs0, ws0);
         issue(x0, w0);
-#pragma unroll
-        for (int n = 0; n < NB; ++n)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[n][r] = 0.f;
         __syncthreads();
+        acc_reset(acc, bias_lds, kBiasInit);
         for (int t = 0; t < ntiles; ++t) {
             float* bnext = bias_lds + ((t + 1) & 1) * kTileF;
             for (int s = 0; s < nds2; s += 2) {
@@ -444,12 +462,9 @@ struct TileStream {
                 __syncthreads();
             }
             float bv[16];
-            bias_read(bv, bias_lds + (t & 1) * kTileF);
+            if (!kBiasInit) bias_read(bv, bias_lds + (t & 1) * kTileF);
             epi(t, acc, bv);
-#pragma unroll
-            for (int n = 0; n < NB; ++n)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[n][r] = 0.f;
+            acc_reset(acc, bias_lds + ((t + 1) & 1) * kTileF, kBiasInit);   // past the last tile: unused
             __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
         }
     }

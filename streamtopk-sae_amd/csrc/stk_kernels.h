@@ -77,8 +77,31 @@ struct MainArgs {
     int32_t* seg_cnt;            // [B][gridDim.x] keys each workgroup left in its segment
     int lq;                      // LDS queue keys per row (even, <= 64; cap >= k + lq)
     int max_rounds;              // bound of the epilogue's spill-and-retry loop
-    uint32_t* err;               // set non-zero if that bound is ever reached
+    uint64_t* err;               // set to `nonce` if that bound is ever reached
+    uint64_t nonce;              // this call's tag (non-zero, unique per call in the process)
+    // Threshold exchange (xch != 0; then thr0 is null and nothing is sampled):
+    // after its first tile every workgroup publishes each row's largest score
+    // of that tile, the owner of a row takes the k-th largest of those maxima
+    // as the row's threshold, and every workgroup reads its rows' thresholds
+    // before its first epilogue filters anything.  Each word: the call's tag
+    // (low 32 bits of nonce) << 32 | a score image (ordered_u32).
+    int xch;
+    uint64_t* xmax;              // [nbc][32*NB][gridDim.x] each workgroup's row maxima
+    uint64_t* xthr;              // [nbc][32*NB] row thresholds (owner x: rows x, x + gridDim.x, ...)
+    int64_t xwait;               // s_memrealtime ticks a wave polls for words before going
+                                 //   on without the exchanged thresholds (threshold 0)
 };
+
+// Row blocks of main_kernel whose workgroups exchange thresholds need at
+// least this many workgroups (an owner workgroup handles its rows one wave
+// each: at most 128 / kXchMinWg <= kMainWaves rows).
+constexpr int kXchMinWg = 16;
+// 2 ms at the 100 MHz s_memrealtime clock: far above the skew of the first
+// tile's end over the grid (microseconds), so reached only if some
+// workgroups were not resident.  The exchange's words are read only after
+// their tag matches the call's; a workspace must therefore be zero-filled
+// before its first use (tag 0 is never a call's).
+constexpr int64_t kXchWaitTicks = 200000;
 
 // Row r's head count is list_cnt[r * kCntStride]: one 128-byte line per row.
 constexpr int kCntStride = 32;
@@ -87,10 +110,12 @@ constexpr int kCntStride = 32;
 // number of rounds.  The bounds are never reached (main_kernel places at least
 // lq >= 8 of a row's <= 256 pending scores per round, mainl_kernel at least
 // cap - k >= 64), so they only guard against a broken invariant: reaching one
-// sets the workspace's error word, and the merge then marks every row of its
-// output (indices -1, values NaN) instead of returning a silently wrong
-// result.  STK_TEST_MAX_ROUNDS=n in the environment allows n spill rounds
-// instead (a test hook that forces that path from the host; 0: none).
+// sets the workspace's error word to the call's nonce, and the merge of that
+// call then marks every row of its output (indices -1, values NaN) instead of
+// returning a silently wrong result.  A word holding another call's nonce (or
+// anything else) means no error: nothing has to clear it between calls.
+// STK_TEST_MAX_ROUNDS=n in the environment allows n spill rounds instead (a
+// test hook that forces that path from the host; 0: none).
 constexpr int kMainMaxRounds = 4096;
 constexpr int kMainLMaxRounds = 1 << 20;
 
@@ -119,7 +144,6 @@ struct ThrArgs {
     uint64_t* list_keys;         // [B][list_cap]: receives the sampled keys >= thr
     int32_t* list_cnt;           // [B * kCntStride] set to the number of those keys
     int64_t list_cap;
-    uint32_t* err;               // the call's error word, cleared by row 0's workgroup
 };
 
 // Large-batch streaming kernel: 256 rows x 256 latents per tile, queues in
@@ -142,7 +166,8 @@ struct MainLArgs {
     int64_t list_cap, head_span;
     int32_t* seg_cnt;            // [B][nr] keys in each segment
     int max_rounds;              // bound of the overflow loop (see kMainLMaxRounds)
-    uint32_t* err;
+    uint64_t* err;               // set to `nonce` if that bound is ever reached
+    uint64_t nonce;
     // sample mode (mainl_sample_kernel): 256-latent tiles of the sampled
     // latents, d split in ksplit ranges; raw partial scores to P
     int ksplit, nsamp;
@@ -171,7 +196,8 @@ struct MergeArgs {
     int32_t f_offset;            // added to every emitted index (a shard's first latent)
     int ties;                    // non-zero: keys may repeat (stk_topk_merge's parts); equal keys
                                  //   take consecutive ranks
-    const uint32_t* err;         // non-zero: mark the output rows (-1, NaN); may be null
+    const uint64_t* err;         // equal to `nonce`: mark the output rows (-1, NaN); may be null
+    uint64_t nonce;
     float* V;
     int32_t* I;
 };

@@ -138,6 +138,161 @@ __device__ __forceinline__ void flush_rows(int* cnt, int* gcnt, uint64_t* thr, c
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the segment stores are complete
 }
 
+// ---------------------------------------------------------------------------
+// Threshold exchange (main_kernel, MainArgs::xch)
+// ---------------------------------------------------------------------------
+// Every word the exchange shares between workgroups carries the call's tag
+// (the low 32 bits of its nonce, never 0) in its high half and its data in
+// the low half, and is written and read whole with agent-scope atomic stores
+// and loads (coherent across the XCDs' L2s word by word).  A reader polls the
+// words it needs until every tag is this call's: no flag has to be ordered
+// after the data, so no writer waits for its stores, and the last poll
+// returns the data.  Words of earlier calls carry other tags; a workspace
+// starts zero-filled, and tag 0 is never used.
+
+// Wave-level: polls n <= 256 words p[0..n) (4 per lane) until at least
+// `need` of them carry `tag`, for at most `wait` ticks of the 100 MHz
+// real-time counter; v[u] receives the low half of word lane + 64 u if it
+// carries the tag, else 0.  Returns whether `need` words arrived (the same in
+// every lane).  wait <= 0: false at once.
+__device__ __forceinline__ bool xch_poll4(const uint64_t* p, int n, int need, uint32_t tag, int64_t wait,
+                                          int lane, uint32_t (&v)[4])
+{
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = 0u;
+    if (wait <= 0) return false;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+        int got = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = lane + 64 * u;
+            bool tagged = false;
+            if (i < n) {
+                const uint64_t w = __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                tagged = (uint32_t)(w >> 32) == tag;
+                v[u] = tagged ? (uint32_t)w : 0u;
+            }
+            got += __popcll(__ballot(tagged));
+        }
+        if (got >= need) return true;
+        if ((int64_t)(__builtin_amdgcn_s_memrealtime() - t0) >= wait) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// After the first tile's scores (bias included) are in ac: fills thr[0..BT)
+// with the row thresholds of the exchange.
+//   1. Each workgroup publishes, per row, the score image (ordered_u32) of
+//      the largest score of its first tile (NaN scores left out).
+//   2. Workgroup x owns rows x, x + nwg, ... of its row block (one wave per
+//      row): once max(k, 3/4 nwg) of the row's maxima have arrived, it takes
+//      the k-th largest of those: at least k distinct latents of the row
+//      score at least that value, so it is a lower bound of the row's k-th
+//      score, whichever maxima arrived first (the result does not depend on
+//      it, only the number of candidates).  Not waiting for the last quarter
+//      spares the workgroups of the slowest XCDs most of the wait.  The
+//      threshold key is the largest key below every key of that score.
+//   3. Every workgroup polls its block's thresholds.
+// A poll that runs out (some workgroup never became resident) leaves the
+// affected thresholds at 0, which accepts every score: the result stays
+// exact, the call only slower.  scr: 8 * BT LDS words, free while the
+// epilogue runs.
+template <int NB>
+__device__ __forceinline__ void xch_thresholds(const MainArgs& a, const f32x16 (&ac)[NB], uint32_t vmask,
+                                               uint64_t* thr, uint32_t* scr, int64_t b0, int tid)
+{
+    constexpr int BT = 32 * NB;
+    const int lane = tid & 63, wave = tid >> 6, h = lane >> 5, jl = lane & 31;
+    const int nwg = (int)gridDim.x, x = (int)blockIdx.x;
+    const int nrows = (int)(a.B - b0 < BT ? a.B - b0 : BT);
+    const int nown = nwg < nrows ? nwg : nrows;
+    const uint32_t tag = (uint32_t)a.nonce;
+    const uint64_t tg = (uint64_t)tag << 32;
+    // the row block passes through an empty asm so that no address derived
+    // from it is hoisted out of the tile loop (kept live, it would spill)
+    int64_t yb = blockIdx.y;
+    asm volatile("" : "+s"(yb));
+    uint64_t* xmax = a.xmax + yb * BT * nwg;   // [BT][nwg]
+    uint64_t* xthr = a.xthr + yb * BT;         // [BT]
+
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+        float m = -__builtin_inff();
+#pragma unroll
+        for (int r = 0; r < 16; ++r) m = __builtin_fmaxf(m, ((vmask >> r) & 1u) ? ac[n][r] : -__builtin_inff());
+        const uint32_t o = ordered_u32(m);
+        const uint32_t q = __shfl_xor(o, 32);
+        if (h == 0) scr[wave * BT + 32 * n + jl] = q > o ? q : o;
+    }
+    __syncthreads();
+    if (tid < nrows) {
+        uint32_t m = scr[tid];
+#pragma unroll
+        for (int w = 1; w < kMainWaves; ++w) {
+            const uint32_t o = scr[w * BT + tid];
+            m = o > m ? o : m;
+        }
+        __hip_atomic_store(xmax + (int64_t)tid * nwg + x, tg | m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    const int row = x + wave * nwg;
+    if (x < nown && row < nrows) {
+        uint32_t v[4];
+        uint32_t T = 0;
+        const int quorum = (3 * nwg + 3) / 4;
+        if (xch_poll4(xmax + (int64_t)row * nwg, nwg, a.k > quorum ? a.k : quorum, tag, a.xwait, lane, v)) {
+            // The k-th largest T* of the arrived maxima lies in [lo, hi], the
+            // smallest and largest of them (at least k arrived), so it shares
+            // their common leading bits; below those T is built bit by bit
+            // (the largest T with at least k maxima >= T) over 12 bits, the
+            // rest left 0.  T <= T*: a lower bound still, at most 2^-11 of
+            // the score below T*.
+            uint32_t lo = ~0u, hi = 0u;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                lo = (v[u] != 0u && v[u] < lo) ? v[u] : lo;
+                hi = v[u] > hi ? v[u] : hi;
+            }
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                const uint32_t l2 = __shfl_xor(lo, off), h2 = __shfl_xor(hi, off);
+                lo = l2 < lo ? l2 : lo;
+                hi = h2 > hi ? h2 : hi;
+            }
+            const uint32_t diff = lo ^ hi;
+            if (diff == 0u) {
+                T = hi;
+            } else {
+                const int top = 31 - __builtin_clz(diff);
+                T = hi & ~((2u << top) - 1u);   // the common leading bits (2u << 31 wraps to 0: none)
+                const int stop = top >= 11 ? top - 11 : 0;
+                for (int bit = top; bit >= stop; --bit) {
+                    const uint32_t c = T | (1u << bit);
+                    int cnt = 0;
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) cnt += __popcll(__ballot(v[u] >= c));
+                    T = cnt >= a.k ? c : T;
+                }
+            }
+        }
+        if (lane == 0) __hip_atomic_store(xthr + row, tg | T, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    // waves 0 and 1 poll the block's thresholds, a row per lane
+    if (wave < 2) {
+        uint32_t v[4];
+        const int base = 64 * wave;
+        const int n = nrows - base < 64 ? nrows - base : 64;
+        const bool ok = n > 0 && xch_poll4(xthr + base, n, n, tag, a.xwait, lane, v);
+        if (base + lane < BT) {
+            const uint32_t T = ok ? v[0] : 0u;
+            thr[base + lane] = T ? ((uint64_t)T << 32) - 1 : 0ull;
+        }
+    }
+    __syncthreads();
+}
+
 template <int DT, int NB>
 __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
 {
@@ -190,7 +345,8 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
     ts.init_x((const unsigned char*)a.X, B, b0, a.d);
 
     f32x16 acc[NB];
-    ts.run(acc, smem, bias_lds, [&](int t, f32x16 (&ac)[NB], const float (&bias_r)[16]) {
+    // the accumulators start at the bias: ac holds the scores at the epilogue
+    ts.template run<true>(acc, smem, bias_lds, [&](int t, f32x16 (&ac)[NB], const float (&)[16]) {
         // latent of accumulator register r of this lane: fl + 8*(r/4) + r%4
         const int64_t tile0 = (ts.tile_begin + t) * (int64_t)kTileLatents;
         const int64_t fl = tile0 + wave * 32 + h * 4;
@@ -206,7 +362,8 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
                 vmask |= ok ? (1u << r) : 0u;
             }
         }
-        // ---- scores (bias added in place) not below the row threshold ----
+        if (a.xch && t == 0) xch_thresholds<NB>(a, ac, vmask, thr, (uint32_t*)(smem + TS::kWBuf), b0, tid);
+        // ---- scores not below the row threshold ----
         // The float test keeps every score whose key beats the threshold key
         // (and possibly a few equal to its value: harmless extra candidates).
         uint32_t pend[NB];
@@ -217,19 +374,16 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
             const float tv = tk ? key_value(tk) : -__builtin_inff();
             uint32_t m = 0;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                ac[n][r] += bias_r[r];
-                m |= (!(ac[n][r] < tv)) ? (1u << r) : 0u;
-            }
+            for (int r = 0; r < 16; ++r) m |= (!(ac[n][r] < tv)) ? (1u << r) : 0u;
             pend[n] = (b0 + j < B) ? (m & vmask) : 0u;
         }
 
         // ---- append to the LDS queues; spill full ones and retry while anything overflowed ----
-        // The second ring buffers are idle during the epilogue: the W one holds
-        // each wave's scores of one row block as [r][lane] (a survivor's score
-        // is one LDS read away: a lane cannot index its own registers), the X
-        // one a slot per thread that absorbs the writes of overflowing survivors.
-        float* sc = (float*)(smem + TS::kWBuf) + wave * 16 * 64;
+        // A survivor's score comes out of its register by pick16 (a lane
+        // cannot index its own registers; survivors are a few per cent of the
+        // scores, so selecting beats staging every score in LDS).  The second
+        // X ring buffer is idle during the epilogue: a slot per thread there
+        // absorbs the writes of overflowing survivors.
         uint64_t* dump = (uint64_t*)(smem + 2 * TS::kWBuf + TS::kXBuf) + tid;
         for (int it = 0;; ++it) {
             bool overflow = false;
@@ -240,9 +394,7 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
                 base[n] = pend[n] ? atomicAdd(&cnt[32 * n + jl], __builtin_popcount(pend[n])) : 0;
 #pragma unroll
             for (int n = 0; n < NB; ++n) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) sc[r * 64 + lane] = ac[n][r];
-                // this lane's survivors only (a few per cent of the scores), lowest register first
+                // this lane's survivors only, lowest register first
                 uint64_t* qj = lqk + (32 * n + jl) * lq;
                 uint32_t m = pend[n], keep = 0;
                 int slot = base[n];
@@ -250,7 +402,7 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
                     const uint32_t r = (uint32_t)__builtin_ctz(m);
                     m &= m - 1u;
                     const bool ok = slot < lq;
-                    *(ok ? qj + slot : dump) = make_key(sc[r * 64 + lane], fl + (r >> 2) * 8 + (r & 3));
+                    *(ok ? qj + slot : dump) = make_key(pick16(ac[n], r), fl + (r >> 2) * 8 + (r & 3));
                     keep |= ok ? 0u : (1u << r);
                     ++slot;
                 }
@@ -261,7 +413,7 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
             if (it >= a.max_rounds) {
                 // unreachable by the bound's argument (kMainMaxRounds): the
                 // pending scores are lost, so the call's result is marked
-                if (tid == 0) atomicOr(a.err, 1u);
+                if (tid == 0) __hip_atomic_store(a.err, a.nonce, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
             __syncthreads();   // the LDS queues are complete
@@ -441,7 +593,6 @@ __global__ __launch_bounds__(NT) void thr_kernel(ThrArgs a)
     __shared__ SelSharedT<NT> S;
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
-    if (row == 0 && tid == 0) *a.err = 0u;   // the first kernel that runs after it is read
     if (a.P == nullptr) {
         if (tid == 0) { a.thr[row] = 0; a.list_cnt[row * kCntStride] = 0; }
         return;
@@ -609,13 +760,14 @@ __device__ __forceinline__ void merge_pass(SelSharedT<NT>& S, const uint64_t (&v
 // at once, unconditionally (clamped into the row's list, masked afterwards),
 // together with the row's count; every other slot is loaded only if it holds
 // a candidate.
-// Whether the call's error word is set (a streaming kernel lost candidates);
-// if so, row `row` of the output is marked: indices -1, values NaN.  The word
-// is the same for every thread, so the whole workgroup returns together.
+// Whether the error word holds this call's nonce (a streaming kernel of the
+// call lost candidates); if so, row `row` of the output is marked: indices
+// -1, values NaN.  The word is the same for every thread, so the whole
+// workgroup returns together.
 template <int NT = kThreads>
 __device__ __forceinline__ bool merge_marked(const MergeArgs& a, int64_t row, int tid)
 {
-    if (a.err == nullptr || *a.err == 0u) return false;
+    if (a.err == nullptr || *a.err != a.nonce) return false;
     for (int r = tid; r < a.k; r += NT) {
         a.V[row * a.k + r] = __builtin_nanf("");
         a.I[row * a.k + r] = -1;
@@ -634,7 +786,7 @@ __global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a)
     if (merge_marked<NT>(a, row, tid)) return;
     const int k = a.k;
     const int nseg = a.nseg;
-    const int64_t hc = a.list_cnt[row * kCntStride];
+    const int64_t hc = a.head_span > 0 ? a.list_cnt[row * kCntStride] : 0;   // no head: no count either
     const uint64_t* keys = a.list_keys + row * a.list_cap;
     uint64_t v[kPer];
 #pragma unroll
@@ -751,7 +903,7 @@ __global__ __launch_bounds__(NT) void merge_seg_kernel(MergeArgs a)
     const uint64_t* keys = a.list_keys + row * a.list_cap;
     uint64_t v[kPer + 1];
     v[kPer] = tid < hs ? keys[tid] : 0ull;   // the head key rides in the first pass
-    const int hc = a.list_cnt[row * kCntStride];
+    const int hc = hs > 0 ? a.list_cnt[row * kCntStride] : 0;
     if (tid == 0) S.cnt = 0;
     uint64_t run = 0;
     for (int s0 = 0; s0 < nseg || s0 == 0; s0 += kThreads) {

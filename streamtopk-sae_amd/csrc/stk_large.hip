@@ -529,7 +529,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                         if (it >= a.max_rounds) {
                             // unreachable by the bound's argument (kMainLMaxRounds):
                             // the pending scores are lost, so the result is marked
-                            if (tid == 0) atomicOr(a.err, 1u);
+                            if (tid == 0) __hip_atomic_store(a.err, a.nonce, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                             break;
                         }
                         __threadfence_block();   // this thread's segment stores are complete

@@ -16,7 +16,9 @@ sees every byte and no (B, F) buffer is ever created.
 The workspace (scratch for the duration of one call) is kept per (device,
 stream) and reused by later calls on that stream, grown when a call needs more:
 calls queued on one stream run one after another, and calls on different
-streams get different workspaces.  ``clear_workspace_cache()`` releases them.
+streams get different workspaces.  A new workspace is zero-filled, as the
+library requires before a workspace's first use; calls leave it valid for the
+next.  ``clear_workspace_cache()`` releases them.
 """
 import ctypes
 import threading
@@ -49,7 +51,7 @@ def _workspace(device, stream, nbytes):
         ws = _WS.get(key)
         if ws is None or ws.numel() < nbytes:
             _WS.pop(key, None)
-            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+            ws = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
             _WS[key] = ws
         return ws
 

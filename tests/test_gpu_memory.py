@@ -12,7 +12,7 @@ asks for, nothing else (the library itself never allocates).  The bounds:
   that exceeds the workspace's F-independent floor, B * #CUs * (k + queue)
   keys: configs 2 and 4.  Config 1 has as many workgroups as tiles (256), so
   its per-workgroup segments of k + lq keys make it 1.4x that figure;
-* the workspace does not grow with F.
+* the workspace is bounded in F.
 """
 import ctypes
 
@@ -73,12 +73,15 @@ def test_peak_memory_bound(cuda_dev, name):
         assert peak <= 1.5 * tiles_k
 
 
-def test_workspace_independent_of_F(cuda_dev):
-    """Past the sample's size the workspace stays flat in F (every row keeps a
-    head and one bounded segment per workgroup, however many tiles each
-    workgroup streams)."""
-    small = _workspace(128, 2048, 1 << 18, 64)
-    big = _workspace(128, 2048, 1 << 22, 64)
-    assert big == small
+def test_workspace_bounded_in_F(cuda_dev):
+    """The workspace is bounded in F: every row keeps one segment per
+    workgroup of k keys plus at most the LDS queue's length, however many
+    tiles each workgroup streams.  Below 512 rows the queue is sized by the
+    survivors a workgroup expects, which grow with its tiles until the queue
+    reaches its LDS limit (by F = 2^22 at config 2's shape); large batches
+    keep a head and fixed segments."""
+    s18 = _workspace(128, 2048, 1 << 18, 64)
+    s22 = _workspace(128, 2048, 1 << 22, 64)
+    assert s18 <= s22 == _workspace(128, 2048, 1 << 26, 64)
     big_b = _workspace(1024, 4096, 1 << 22, 128)
     assert big_b == _workspace(1024, 4096, 1 << 18, 128)

@@ -1,0 +1,141 @@
+"""GPU tests of main_kernel's threshold exchange (batches below 512 rows).
+
+Without a sample pass, every main_kernel workgroup publishes the largest key
+of each row in its first tile; the owner of a row takes the k-th largest of
+those maxima as the row's threshold, and every workgroup reads its rows'
+thresholds before its first epilogue filters anything.  The flags that order
+this carry a per-call nonce, and every wait is bounded: a wait that runs out
+leaves threshold 0 (every score a candidate), so the result stays exact.
+
+Checked here: which kernels a call launches (the exchange replaces the
+sample and threshold passes when the grid has at least max(k, 16)
+workgroups), exact results with every wait forced to run out at once
+(STK_TEST_XCH_WAIT=0, read by the library at each call), back-to-back calls
+on one cached workspace with different inputs and shapes (stale flags and
+maxima of an earlier call must never be taken for this call's), and score
+distributions that defeat the threshold (all scores equal, all the best
+latents in one workgroup's range).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from parity import check_against_scores, tol_of
+from streamtopk_sae import _lib, make_inputs, topk_sae_cuda_exact
+
+pytestmark = pytest.mark.gpu
+
+DT = {"fp32": torch.float32, "fp16": torch.float16, "bf16": torch.bfloat16}
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _check(X, W, b, k, dtype_name, name):
+    V, I = topk_sae_cuda_exact(X, W, b, k)
+    torch.cuda.synchronize()
+    S = oracle.scores_f64(_np(X), _np(W), _np(b))
+    check_against_scores(V.cpu().numpy(), I.cpu().numpy(), S, k, tol_of(dtype_name), name)
+    return V, I
+
+
+def _launches(fn):
+    """Kernel launches of fn() by name, from the library's per-kernel event records."""
+    lib = _lib.load()
+    _lib.check(lib.stk_profile_enable(1))
+    try:
+        fn()
+        torch.cuda.synchronize()
+        out = {}
+        for name in ("sample_kernel", "thr_kernel", "main_kernel", "merge_kernel"):
+            tot = ctypes.c_double(0.0)
+            n = ctypes.c_int64(0)
+            _lib.check(lib.stk_profile_read(name.encode(), ctypes.byref(tot), ctypes.byref(n)))
+            out[name] = n.value
+        return out
+    finally:
+        _lib.check(lib.stk_profile_enable(0))
+
+
+@pytest.mark.parametrize("B,F,k,xch", [
+    (128, 65536, 32, True),      # config 1's shape: 256 workgroups
+    (40, 16384 + 37, 64, True),  # 65 tiles, 65 workgroups >= k
+    (40, 16384 + 37, 128, False),  # 65 workgroups < k: the sample pass seeds the thresholds
+    (600, 65536, 64, False),     # large batch: mainl_kernel with its sample pass
+])
+def test_exchange_replaces_threshold_passes(cuda_dev, B, F, k, xch):
+    print(f"case launches B={B} F={F} k={k}", flush=True)
+    X, W, b = make_inputs(B, 128, F, torch.bfloat16, seed=11, device=cuda_dev)
+    n = _launches(lambda: topk_sae_cuda_exact(X, W, b, k))
+    assert n["main_kernel"] == 1 and n["merge_kernel"] == 1, n
+    if xch:
+        assert n["sample_kernel"] == 0 and n["thr_kernel"] == 0, n
+    else:
+        assert n["sample_kernel"] == 1 and n["thr_kernel"] == 1, n
+
+
+@pytest.mark.parametrize("B,d,F,k,dtype_name", [
+    (1, 64, 8192, 16, "bf16"),
+    (64, 256, 65536, 64, "bf16"),
+    (128, 128, 40000, 128, "fp16"),
+    (300, 96, 30000, 32, "fp32"),   # three row blocks, each its own exchange
+])
+def test_exchange_waits_run_out(cuda_dev, monkeypatch, B, d, F, k, dtype_name):
+    """Every exchange wait runs out at once: thresholds stay 0 and the result is still exact."""
+    print(f"case xch timeout B={B} d={d} F={F} k={k} {dtype_name}", flush=True)
+    X, W, b = make_inputs(B, d, F, DT[dtype_name], seed=12, device=cuda_dev)
+    monkeypatch.setenv("STK_TEST_XCH_WAIT", "0")
+    V0, I0 = _check(X, W, b, k, dtype_name, "waits run out")
+    monkeypatch.delenv("STK_TEST_XCH_WAIT")
+    V1, I1 = _check(X, W, b, k, dtype_name, "exchange")
+    assert torch.equal(I0, I1) and torch.equal(V0, V1)
+
+
+def test_back_to_back_calls(cuda_dev):
+    """Calls on one cached workspace, inputs and shapes changing from call to
+    call with no synchronisation between them: each result matches its own
+    inputs.  A stale flag or maximum of an earlier call taken for this call's
+    would raise a threshold above the row's k-th score and drop answers."""
+    print("case back-to-back", flush=True)
+    cases = []
+    for i, (B, F, k) in enumerate([(128, 65536, 32), (128, 65536, 32), (96, 50000, 64),
+                                   (128, 65536, 32), (33, 65536, 16), (128, 65536, 32)]):
+        X, W, b = make_inputs(B, 128, F, torch.bfloat16, seed=100 + i, device=cuda_dev)
+        if i == 3:
+            # the previous maxima would now be far too high thresholds
+            X = X * 1e-3
+        cases.append((X, W, b, k))
+    outs = [topk_sae_cuda_exact(X, W, b, k) for X, W, b, k in cases]
+    torch.cuda.synchronize()
+    for i, ((X, W, b, k), (V, I)) in enumerate(zip(cases, outs)):
+        S = oracle.scores_f64(_np(X), _np(W), _np(b))
+        check_against_scores(V.cpu().numpy(), I.cpu().numpy(), S, k, tol_of("bf16"), f"call {i}")
+
+
+def test_all_scores_equal(cuda_dev):
+    """Every score equal: the threshold accepts every latent (ties at its
+    value are candidates), and the lower index wins among equals."""
+    print("case all-equal", flush=True)
+    B, d, F, k = 64, 64, 65536, 64
+    X = torch.zeros(B, d, dtype=torch.bfloat16, device=cuda_dev)
+    W = torch.ones(F, d, dtype=torch.bfloat16, device=cuda_dev)
+    b = torch.full((F,), 0.25, dtype=torch.float32, device=cuda_dev)
+    V, I = topk_sae_cuda_exact(X, W, b, k)
+    assert torch.equal(I.cpu(), torch.arange(k, dtype=torch.int32).expand(B, k))
+    assert bool((V == 0.25).all())
+
+
+def test_best_latents_in_one_workgroup(cuda_dev):
+    """All of a row's best latents inside one workgroup's range of tiles: the
+    exchanged threshold is low for them and that workgroup's queues spill;
+    the answer is still exact."""
+    print("case clustered", flush=True)
+    B, d, F, k = 128, 128, 262144, 128
+    X, W, b = make_inputs(B, d, F, torch.bfloat16, seed=13, device=cuda_dev)
+    b = b.clone()
+    b[5000:5000 + 2 * k] += 50.0
+    _check(X, W, b, k, "bf16", "clustered")

@@ -35,7 +35,7 @@ def _with_workspace(X, W, b, k):
     F = W.shape[0]
     nb = ctypes.c_size_t(0)
     _lib.check(lib.stk_exact_workspace_bytes(B, d, F, k, _lib.STK_DTYPE_BF16, ctypes.byref(nb)))
-    ws = torch.empty(nb.value, dtype=torch.uint8, device=X.device)
+    ws = torch.zeros(nb.value, dtype=torch.uint8, device=X.device)   # zero-filled before first use
     V, I = _outputs(B, k, X.device)
     _lib.check(lib.stk_exact_forward(_p(X), _p(W), _p(b), _p(V), _p(I), B, d, F, k, _lib.STK_DTYPE_BF16,
                                      _p(ws), nb.value, _stream()))
