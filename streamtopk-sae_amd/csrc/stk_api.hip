@@ -493,10 +493,11 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         mg.list_keys = list_keys; mg.list_cnt = list_cnt; mg.list_cap = p.list_cap;
         mg.head_span = p.head_span; mg.nseg = p.nwg; mg.seg_cap = p.cap; mg.seg_cnt = seg_cnt;
         // the head holds at most k keys (nsamp <= kSelCap) or none: two
-        // merge threads per segment, read in place, in passes of 32 keys
-        // where a segment expects at most ~12, of 48 up to ~24, else of 64
+        // merge threads per segment, read in place, in passes of 8 keys where
+        // a segment expects at most ~3 (the exchange at c1 and c2), of 32 up
+        // to ~12, of 48 up to ~24, else of 64
         const int64_t per_seg = p.expect_seg;
-        mg.spec = per_seg <= 12 ? 3 : per_seg <= 24 ? 4 : 5;
+        mg.spec = per_seg <= 3 ? 6 : per_seg <= 12 ? 3 : per_seg <= 24 ? 4 : 5;
     }
     mg.k = (int)k;
     mg.f_offset = (int32_t)f_offset;

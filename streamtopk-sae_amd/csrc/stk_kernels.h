@@ -191,8 +191,8 @@ struct MergeArgs {
     int spec;                    // 0: chunks of 16 candidates per thread; a list
                                  //   expected to hold more than 4096 candidates
                                  //   (32 per thread and chunk): 1 dense, 2 segmented;
-                                 //   3, 4, 5: merge_seg_kernel (head <= 256 keys, two
-                                 //   threads per segment; 32, 48 or 64 keys per pass)
+                                 //   6, 3, 4, 5: merge_seg_kernel (head <= 256 keys, two
+                                 //   threads per segment; 8, 32, 48 or 64 keys per pass)
     int32_t f_offset;            // added to every emitted index (a shard's first latent)
     int ties;                    // non-zero: keys may repeat (stk_topk_merge's parts); equal keys
                                  //   take consecutive ranks

@@ -1132,6 +1132,8 @@ hipError_t launch_merge(const MergeArgs& a, int64_t rows, hipStream_t st)
         launch(merge_kernel<32, 16, kThreads>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     else if (a.spec == 2)
         launch(merge_kernel<32, 0, kThreads>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+    else if (a.spec == 6)   // segments expected to hold up to ~3 keys: 8 per pass
+        launch(merge_seg_kernel<4, 4, 2 * kThreads>, dim3((unsigned)rows), dim3(2 * kThreads), 0, st, a);
     else if (a.spec == 3)   // segments expected to hold up to ~12 keys: 32 per pass
         launch(merge_seg_kernel<16, 8, 2 * kThreads>, dim3((unsigned)rows), dim3(2 * kThreads), 0, st, a);
     else if (a.spec == 4)   // segments expected to hold up to ~24 keys: 48 per pass

@@ -59,8 +59,8 @@ def test_every_kernel_without_scratch(asm):
 def test_selection_kernels_at_512_threads(asm):
     names = _kernels(asm)
     wide = [n for n in names if ("merge_seg_kernel" in n or "thr_kernel" in n) and "Li512E" in n]
-    # the three merge widths and the large sample's threshold
-    assert len(wide) == 4, wide
+    # the four merge widths and the large sample's threshold
+    assert len(wide) == 5, wide
 
 
 def test_main_kernel_registers(asm):
