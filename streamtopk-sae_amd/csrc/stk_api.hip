@@ -227,8 +227,14 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
     // Without a large batch, the first tile of every workgroup seeds the
     // thresholds (each row's k-th largest of the workgroups' maxima) when
     // there are enough workgroups for a k-th; otherwise a sample pass does.
-    // (STK_TEST_NO_XCH, a test hook read at each call, selects the sample pass)
-    p.xch = !p.large && p.nwg >= kXchMinWg && p.nwg >= k && p.nwg <= 256 && !std::getenv("STK_TEST_NO_XCH");
+    // (STK_TEST_NO_XCH, a test hook read at each call, selects the sample pass).
+    // Large batches exchange kLXchPerWg maxima per row and workgroup (nwg = the
+    // W ranges per row block), up to 512 per row.
+    if (p.large)
+        p.xch = (int64_t)p.nwg * kLXchPerWg >= k && p.nwg * kLXchPerWg <= 512;
+    else
+        p.xch = p.nwg >= kXchMinWg && p.nwg >= k && p.nwg <= 256;
+    if (std::getenv("STK_TEST_NO_XCH")) p.xch = false;
     p.sample = F >= kSampleMinF && !p.xch;
     p.samp_log2 = 0;
     p.nsamp = 0;
@@ -319,9 +325,11 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
     off = align256(off + (size_t)B * p.list_cap * 8);
     p.off_xmax = p.off_xthr = off;
     if (p.xch) {
-        const size_t bt = 32 * (size_t)p.NB;
+        // [nbc][bt][words per row]
+        const size_t bt = p.large ? (size_t)kLargeRows : 32 * (size_t)p.NB;
+        const size_t per_row = p.large ? (size_t)p.nwg * kLXchPerWg : (size_t)p.nwg;
         p.off_xmax = off;
-        off = align256(off + (size_t)p.nbc * p.nwg * bt * 8);
+        off = align256(off + (size_t)p.nbc * bt * per_row * 8);
         p.off_xthr = off;
         off = align256(off + (size_t)p.nbc * bt * 8);
     }
@@ -450,7 +458,7 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         ml.k = (int)k; ml.cap = p.cap;
         ml.num_tiles = p.num_tiles; ml.tiles_per_wg = p.tpw;
         ml.nbc = (int)p.nbc; ml.nr = p.nwg;
-        ml.thr0 = thr;
+        ml.thr0 = p.xch ? nullptr : thr;
         ml.sampled = p.sample ? 1 : 0;
         ml.samp_log2 = p.samp_log2;
         ml.samp_blocks = p.nsamp / kSampleBlock;
@@ -459,6 +467,10 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         ml.max_rounds = max_rounds >= 0 ? max_rounds : kMainLMaxRounds;
         ml.err = err;
         ml.nonce = nonce;
+        ml.xch = p.xch ? 1 : 0;
+        ml.xmax = (uint64_t*)(ws + p.off_xmax);
+        ml.xthr = (uint64_t*)(ws + p.off_xthr);
+        ml.xwait = xwait;
         int pm = prof_begin("main_kernel", st);
         e = launch_mainl(dt, ml, (int)(p.nbc * p.nwg), st);
         prof_end(pm, st);

@@ -74,6 +74,97 @@ __device__ __forceinline__ uint64_t make_key(float v, int64_t idx)
     return ((uint64_t)ordered_u32(v) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)idx);
 }
 
+// ---------------------------------------------------------------------------
+// Threshold exchange helpers (main_kernel, mainl_kernel).  Every word the
+// workgroups of one call share carries the call's tag (the low 32 bits of its
+// nonce, never 0) in its high half and its data in the low half, and is
+// written and read whole with agent-scope atomic stores and loads (coherent
+// across the XCDs' L2s word by word).  A reader polls the words it needs
+// until enough carry the call's tag: no flag has to be ordered after the
+// data, so no writer waits for its stores, and the last poll returns the
+// data.  Words of earlier calls carry other tags; a workspace starts
+// zero-filled, and tag 0 is never used.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void xch_put(uint64_t* p, uint32_t tag, uint32_t data)
+{
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | data, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wave-level: polls n <= 64 * U words p[0..n) (U per lane) until at least
+// `need` of them carry `tag`, for at most `wait` ticks of the 100 MHz
+// real-time counter; v[u] receives the low half of word lane + 64 u if it
+// carries the tag, else 0.  Returns whether `need` words arrived (the same in
+// every lane).  wait <= 0: false at once.
+template <int U>
+__device__ __forceinline__ bool xch_poll(const uint64_t* p, int n, int need, uint32_t tag, int64_t wait, int lane,
+                                         uint32_t (&v)[U])
+{
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = 0u;
+    if (wait <= 0) return false;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+        int got = 0;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = lane + 64 * u;
+            bool tagged = false;
+            if (i < n) {
+                const uint64_t w = __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                tagged = (uint32_t)(w >> 32) == tag;
+                v[u] = tagged ? (uint32_t)w : 0u;
+            }
+            got += __popcll(__ballot(tagged));
+        }
+        if (got >= need) return true;
+        if ((int64_t)(__builtin_amdgcn_s_memrealtime() - t0) >= wait) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Wave-level: a lower bound T of the k-th largest of the wave's non-zero
+// values v (at least k of them), T <= T*, the exact k-th largest.  T* lies in
+// [lo, hi], the smallest and largest non-zero values, so it shares their
+// common leading bits; below those T is built bit by bit (the largest T with
+// at least k values >= T) over 12 bits, the rest left 0: at most 2^-11 of a
+// score image below T*.  The same in every lane.
+template <int U>
+__device__ __forceinline__ uint32_t xch_kth(const uint32_t (&v)[U], int k)
+{
+    uint32_t lo = ~0u, hi = 0u;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        lo = (v[u] != 0u && v[u] < lo) ? v[u] : lo;
+        hi = v[u] > hi ? v[u] : hi;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t l2 = __shfl_xor(lo, off), h2 = __shfl_xor(hi, off);
+        lo = l2 < lo ? l2 : lo;
+        hi = h2 > hi ? h2 : hi;
+    }
+    const uint32_t diff = lo ^ hi;
+    if (diff == 0u) return hi;
+    const int top = 31 - __builtin_clz(diff);
+    uint32_t T = hi & ~((2u << top) - 1u);   // the common leading bits (2u << 31 wraps to 0: none)
+    const int stop = top >= 11 ? top - 11 : 0;
+    for (int bit = top; bit >= stop; --bit) {
+        const uint32_t c = T | (1u << bit);
+        int cnt = 0;
+#pragma unroll
+        for (int u = 0; u < U; ++u) cnt += __popcll(__ballot(v[u] >= c));
+        T = cnt >= k ? c : T;
+    }
+    return T;
+}
+
+// The threshold key of score image T: the largest key below every key of
+// that score (0, accept everything, for T = 0).
+__device__ __forceinline__ uint64_t xch_key(uint32_t T)
+{
+    return T ? ((uint64_t)T << 32) - 1 : 0ull;
+}
+
 // Buffer resource (raw, gfx9 family): loads at byte offsets >= num_records
 // return zeros, which bounds rows past B and latents past F, and a zero-length
 // resource makes whole steps read as zeros.

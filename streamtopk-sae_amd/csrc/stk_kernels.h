@@ -151,6 +151,7 @@ struct ThrArgs {
 constexpr int kLargeRows = 256;
 constexpr int kLargeThreads = 256;
 constexpr int64_t kLargeMinB = 512;   // batches from this size use mainl_kernel
+constexpr int kLXchPerWg = 4;         // exchanged maxima per row and mainl_kernel workgroup
 
 struct MainLArgs {
     const void* X;
@@ -168,6 +169,13 @@ struct MainLArgs {
     int max_rounds;              // bound of the overflow loop (see kMainLMaxRounds)
     uint64_t* err;               // set to `nonce` if that bound is ever reached
     uint64_t nonce;
+    // Threshold exchange (xch != 0; then thr0 is null and nothing is sampled),
+    // as MainArgs's, with kLXchPerWg maxima per row and workgroup (one per 64
+    // latents of the first tile).  Tagged words as MainArgs's.
+    int xch;
+    uint64_t* xmax;              // [nbc][kLargeRows][nr * kLXchPerWg]
+    uint64_t* xthr;              // [nbc][kLargeRows]
+    int64_t xwait;
     // sample mode (mainl_sample_kernel): 256-latent tiles of the sampled
     // latents, d split in ksplit ranges; raw partial scores to P
     int ksplit, nsamp;

@@ -141,46 +141,6 @@ __device__ __forceinline__ void flush_rows(int* cnt, int* gcnt, uint64_t* thr, c
 // ---------------------------------------------------------------------------
 // Threshold exchange (main_kernel, MainArgs::xch)
 // ---------------------------------------------------------------------------
-// Every word the exchange shares between workgroups carries the call's tag
-// (the low 32 bits of its nonce, never 0) in its high half and its data in
-// the low half, and is written and read whole with agent-scope atomic stores
-// and loads (coherent across the XCDs' L2s word by word).  A reader polls the
-// words it needs until every tag is this call's: no flag has to be ordered
-// after the data, so no writer waits for its stores, and the last poll
-// returns the data.  Words of earlier calls carry other tags; a workspace
-// starts zero-filled, and tag 0 is never used.
-
-// Wave-level: polls n <= 256 words p[0..n) (4 per lane) until at least
-// `need` of them carry `tag`, for at most `wait` ticks of the 100 MHz
-// real-time counter; v[u] receives the low half of word lane + 64 u if it
-// carries the tag, else 0.  Returns whether `need` words arrived (the same in
-// every lane).  wait <= 0: false at once.
-__device__ __forceinline__ bool xch_poll4(const uint64_t* p, int n, int need, uint32_t tag, int64_t wait,
-                                          int lane, uint32_t (&v)[4])
-{
-#pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = 0u;
-    if (wait <= 0) return false;
-    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    for (;;) {
-        int got = 0;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int i = lane + 64 * u;
-            bool tagged = false;
-            if (i < n) {
-                const uint64_t w = __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                tagged = (uint32_t)(w >> 32) == tag;
-                v[u] = tagged ? (uint32_t)w : 0u;
-            }
-            got += __popcll(__ballot(tagged));
-        }
-        if (got >= need) return true;
-        if ((int64_t)(__builtin_amdgcn_s_memrealtime() - t0) >= wait) return false;
-        __builtin_amdgcn_s_sleep(1);
-    }
-}
-
 // After the first tile's scores (bias included) are in ac: fills thr[0..BT)
 // with the row thresholds of the exchange.
 //   1. Each workgroup publishes, per row, the score image (ordered_u32) of
@@ -208,7 +168,6 @@ __device__ __forceinline__ void xch_thresholds(const MainArgs& a, const f32x16 (
     const int nrows = (int)(a.B - b0 < BT ? a.B - b0 : BT);
     const int nown = nwg < nrows ? nwg : nrows;
     const uint32_t tag = (uint32_t)a.nonce;
-    const uint64_t tg = (uint64_t)tag << 32;
     // the row block passes through an empty asm so that no address derived
     // from it is hoisted out of the tile loop (kept live, it would spill)
     int64_t yb = blockIdx.y;
@@ -233,7 +192,7 @@ __device__ __forceinline__ void xch_thresholds(const MainArgs& a, const f32x16 (
             const uint32_t o = scr[w * BT + tid];
             m = o > m ? o : m;
         }
-        __hip_atomic_store(xmax + (int64_t)tid * nwg + x, tg | m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        xch_put(xmax + (int64_t)tid * nwg + x, tag, m);
     }
 
     const int row = x + wave * nwg;
@@ -241,42 +200,9 @@ __device__ __forceinline__ void xch_thresholds(const MainArgs& a, const f32x16 (
         uint32_t v[4];
         uint32_t T = 0;
         const int quorum = (3 * nwg + 3) / 4;
-        if (xch_poll4(xmax + (int64_t)row * nwg, nwg, a.k > quorum ? a.k : quorum, tag, a.xwait, lane, v)) {
-            // The k-th largest T* of the arrived maxima lies in [lo, hi], the
-            // smallest and largest of them (at least k arrived), so it shares
-            // their common leading bits; below those T is built bit by bit
-            // (the largest T with at least k maxima >= T) over 12 bits, the
-            // rest left 0.  T <= T*: a lower bound still, at most 2^-11 of
-            // the score below T*.
-            uint32_t lo = ~0u, hi = 0u;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                lo = (v[u] != 0u && v[u] < lo) ? v[u] : lo;
-                hi = v[u] > hi ? v[u] : hi;
-            }
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                const uint32_t l2 = __shfl_xor(lo, off), h2 = __shfl_xor(hi, off);
-                lo = l2 < lo ? l2 : lo;
-                hi = h2 > hi ? h2 : hi;
-            }
-            const uint32_t diff = lo ^ hi;
-            if (diff == 0u) {
-                T = hi;
-            } else {
-                const int top = 31 - __builtin_clz(diff);
-                T = hi & ~((2u << top) - 1u);   // the common leading bits (2u << 31 wraps to 0: none)
-                const int stop = top >= 11 ? top - 11 : 0;
-                for (int bit = top; bit >= stop; --bit) {
-                    const uint32_t c = T | (1u << bit);
-                    int cnt = 0;
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) cnt += __popcll(__ballot(v[u] >= c));
-                    T = cnt >= a.k ? c : T;
-                }
-            }
-        }
-        if (lane == 0) __hip_atomic_store(xthr + row, tg | T, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (xch_poll<4>(xmax + (int64_t)row * nwg, nwg, a.k > quorum ? a.k : quorum, tag, a.xwait, lane, v))
+            T = xch_kth<4>(v, a.k);
+        if (lane == 0) xch_put(xthr + row, tag, T);
     }
 
     // waves 0 and 1 poll the block's thresholds, a row per lane
@@ -284,11 +210,8 @@ __device__ __forceinline__ void xch_thresholds(const MainArgs& a, const f32x16 (
         uint32_t v[4];
         const int base = 64 * wave;
         const int n = nrows - base < 64 ? nrows - base : 64;
-        const bool ok = n > 0 && xch_poll4(xthr + base, n, n, tag, a.xwait, lane, v);
-        if (base + lane < BT) {
-            const uint32_t T = ok ? v[0] : 0u;
-            thr[base + lane] = T ? ((uint64_t)T << 32) - 1 : 0ull;
-        }
+        const bool ok = n > 0 && xch_poll<4>(xthr + base, n, n, tag, a.xwait, lane, v);
+        if (base + lane < BT) thr[base + lane] = xch_key(ok ? v[0] : 0u);
     }
     __syncthreads();
 }

@@ -307,7 +307,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
         for (int i = tid; i < kLargeRows; i += kLargeThreads) {
             const int64_t row = b0 + i;
             cnt[i] = 0;
-            thr[i] = (row < B) ? a.thr0[row] : 0ull;
+            thr[i] = (row < B && a.thr0 != nullptr) ? a.thr0[row] : 0ull;
             qrow[i] = (gu64*)(a.list_keys + ((row < B) ? row : 0) * a.list_cap + a.head_span + (int64_t)rg * cap);
         }
     }
@@ -505,6 +505,65 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                 __builtin_amdgcn_wave_barrier();
                 return mm;
             };
+            if (a.xch && t == 0) {
+                // ---- threshold exchange after the first tile (MainArgs::xch's,
+                // with kLXchPerWg maxima per row and workgroup) ----
+                const uint32_t tag = (uint32_t)a.nonce;
+                const int nw = a.nr * kLXchPerWg;   // maxima per row, <= 512 (host)
+                const int nrows = (int)(B - b0 < kLargeRows ? B - b0 : kLargeRows);
+                // the row block passes through an empty asm so that no address
+                // derived from it is hoisted out of the tile loop
+                int64_t rbl = rb;
+                asm volatile("" : "+s"(rbl));
+                uint64_t* xmax = a.xmax + rbl * kLargeRows * nw;   // [kLargeRows][nw]
+                uint64_t* xthr = a.xthr + rbl * kLargeRows;        // [kLargeRows]
+                // 1. per row of this wave, the largest score (NaN left out) of
+                //    each 64-latent half of its 128 latents
+                static_for<kLNB>([&](auto nc) {
+                    constexpr int n = decltype(nc)::value;
+                    const int row = rw0 + 32 * n + jl;
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) {
+                        float m = -__builtin_inff();
+#pragma unroll
+                        for (int f2 = 0; f2 < 2; ++f2) {
+                            const int fa = 2 * q + f2;
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) {
+                                const float v = agpr_read(acc[fa][n][r]) + bias_r[fa * 4 + (r >> 2)][r & 3];
+                                m = __builtin_fmaxf(m, ((vmask >> (16 * fa + r)) & 1ull) ? v : -__builtin_inff());
+                            }
+                        }
+                        uint32_t o = ordered_u32(m);
+                        const uint32_t o2 = __shfl_xor(o, 32);
+                        o = o2 > o ? o2 : o;
+                        if (h == 0 && row < nrows)
+                            xch_put(xmax + (int64_t)row * nw + rg * kLXchPerWg + (wave & 1) * 2 + q, tag, o);
+                    }
+                });
+                // 2. owned rows rg, rg + nr, ...: the k-th largest of the
+                //    row's maxima once max(k, 3/4 nw) have arrived
+                const int quorum = (3 * nw + 3) / 4;
+                const int need = a.k > quorum ? a.k : quorum;
+                for (int j = wave;; j += kLWaves) {
+                    const int row = rg + j * a.nr;
+                    if (row >= nrows) break;
+                    uint32_t v[8];
+                    uint32_t T = 0;
+                    if (xch_poll<8>(xmax + (int64_t)row * nw, nw, need, tag, a.xwait, lane, v))
+                        T = xch_kth<8>(v, a.k);
+                    if (lane == 0) xch_put(xthr + row, tag, T);
+                }
+                // 3. wave w reads rows 64 w .. 64 w + 63
+                {
+                    uint32_t v[1];
+                    const int base = 64 * wave;
+                    const int n = nrows - base < 64 ? nrows - base : 64;
+                    const bool ok = n > 0 && xch_poll<1>(xthr + base, n, n, tag, a.xwait, lane, v);
+                    thr[base + lane] = xch_key(ok ? v[0] : 0u);
+                }
+                __syncthreads();
+            }
             uint64_t ovf[kLNB];
             static_for<kLNB>([&](auto nc) {
                 constexpr int n = decltype(nc)::value;

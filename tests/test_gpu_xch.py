@@ -1,18 +1,20 @@
-"""GPU tests of main_kernel's threshold exchange (batches below 512 rows).
+"""GPU tests of the streaming kernels' threshold exchange.
 
-Without a sample pass, every main_kernel workgroup publishes the largest key
-of each row in its first tile; the owner of a row takes the k-th largest of
-those maxima as the row's threshold, and every workgroup reads its rows'
-thresholds before its first epilogue filters anything.  The flags that order
-this carry a per-call nonce, and every wait is bounded: a wait that runs out
-leaves threshold 0 (every score a candidate), so the result stays exact.
+Without a sample pass, every main_kernel workgroup publishes the largest score
+of each row in its first tile (mainl_kernel, for 512 rows and more: one per 64
+latents of it); the owner of a row takes the k-th largest of those maxima as
+the row's threshold, and every workgroup reads its rows' thresholds before
+its first epilogue filters anything.  Every shared word carries the call's
+tag beside its data, and every poll is bounded: a poll that runs out leaves
+threshold 0 (every score a candidate), so the result stays exact.
 
 Checked here: which kernels a call launches (the exchange replaces the
 sample and threshold passes when the grid has at least max(k, 16)
-workgroups), exact results with every wait forced to run out at once
+workgroups per row block, or, for 512 rows and more, 4 maxima per row and W
+range reach k), exact results with every wait forced to run out at once
 (STK_TEST_XCH_WAIT=0, read by the library at each call), back-to-back calls
-on one cached workspace with different inputs and shapes (stale flags and
-maxima of an earlier call must never be taken for this call's), and score
+on one cached workspace with different inputs and shapes (stale maxima and
+thresholds of an earlier call must never be taken for this call's), and score
 distributions that defeat the threshold (all scores equal, all the best
 latents in one workgroup's range).
 """
@@ -65,11 +67,12 @@ def _launches(fn):
     (128, 65536, 32, True),      # config 1's shape: 256 workgroups
     (40, 16384 + 37, 64, True),  # 65 tiles, 65 workgroups >= k
     (40, 16384 + 37, 128, False),  # 65 workgroups < k: the sample pass seeds the thresholds
-    (600, 65536, 64, False),     # large batch: mainl_kernel with its sample pass
+    (600, 65536, 64, True),      # large batch: mainl_kernel, 80 W ranges x 4 maxima per row
+    (4096, 65536, 128, False),   # 16 W ranges x 4 maxima < k: mainl_kernel with a sample pass
 ])
 def test_exchange_replaces_threshold_passes(cuda_dev, B, F, k, xch):
     print(f"case launches B={B} F={F} k={k}", flush=True)
-    X, W, b = make_inputs(B, 128, F, torch.bfloat16, seed=11, device=cuda_dev)
+    X, W, b = make_inputs(B, 64 if B > 1024 else 128, F, torch.bfloat16, seed=11, device=cuda_dev)
     n = _launches(lambda: topk_sae_cuda_exact(X, W, b, k))
     assert n["main_kernel"] == 1 and n["merge_kernel"] == 1, n
     if xch:
@@ -83,6 +86,8 @@ def test_exchange_replaces_threshold_passes(cuda_dev, B, F, k, xch):
     (64, 256, 65536, 64, "bf16"),
     (128, 128, 40000, 128, "fp16"),
     (300, 96, 30000, 32, "fp32"),   # three row blocks, each its own exchange
+    (600, 128, 30000, 64, "bf16"),  # mainl_kernel, three row blocks
+    (1024, 256, 65536, 128, "fp16"),
 ])
 def test_exchange_waits_run_out(cuda_dev, monkeypatch, B, d, F, k, dtype_name):
     """Every exchange wait runs out at once: thresholds stay 0 and the result is still exact."""
@@ -98,8 +103,8 @@ def test_exchange_waits_run_out(cuda_dev, monkeypatch, B, d, F, k, dtype_name):
 def test_back_to_back_calls(cuda_dev):
     """Calls on one cached workspace, inputs and shapes changing from call to
     call with no synchronisation between them: each result matches its own
-    inputs.  A stale flag or maximum of an earlier call taken for this call's
-    would raise a threshold above the row's k-th score and drop answers."""
+    inputs.  A stale maximum or threshold of an earlier call taken for this
+    call's would raise a threshold above the row's k-th score and drop answers."""
     print("case back-to-back", flush=True)
     cases = []
     for i, (B, F, k) in enumerate([(128, 65536, 32), (128, 65536, 32), (96, 50000, 64),
@@ -109,6 +114,9 @@ def test_back_to_back_calls(cuda_dev):
             # the previous maxima would now be far too high thresholds
             X = X * 1e-3
         cases.append((X, W, b, k))
+    for i, (B, F, k) in enumerate([(600, 40000, 64), (1024, 65536, 128), (600, 40000, 64)]):
+        X, W, b = make_inputs(B, 128, F, torch.bfloat16, seed=200 + i, device=cuda_dev)
+        cases.append((X * (1e-3 if i == 2 else 1.0), W, b, k))
     outs = [topk_sae_cuda_exact(X, W, b, k) for X, W, b, k in cases]
     torch.cuda.synchronize()
     for i, ((X, W, b, k), (V, I)) in enumerate(zip(cases, outs)):
@@ -129,6 +137,18 @@ def test_all_scores_equal(cuda_dev):
     assert bool((V == 0.25).all())
 
 
+def test_all_scores_equal_large_batch(cuda_dev):
+    """As test_all_scores_equal, through mainl_kernel's exchange."""
+    print("case all-equal large", flush=True)
+    B, d, F, k = 512, 64, 65536, 128
+    X = torch.zeros(B, d, dtype=torch.bfloat16, device=cuda_dev)
+    W = torch.ones(F, d, dtype=torch.bfloat16, device=cuda_dev)
+    b = torch.full((F,), -1.5, dtype=torch.float32, device=cuda_dev)
+    V, I = topk_sae_cuda_exact(X, W, b, k)
+    assert torch.equal(I.cpu(), torch.arange(k, dtype=torch.int32).expand(B, k))
+    assert bool((V == -1.5).all())
+
+
 def test_best_latents_in_one_workgroup(cuda_dev):
     """All of a row's best latents inside one workgroup's range of tiles: the
     exchanged threshold is low for them and that workgroup's queues spill;
@@ -139,3 +159,13 @@ def test_best_latents_in_one_workgroup(cuda_dev):
     b = b.clone()
     b[5000:5000 + 2 * k] += 50.0
     _check(X, W, b, k, "bf16", "clustered")
+
+
+def test_best_latents_in_one_w_range_large_batch(cuda_dev):
+    """As test_best_latents_in_one_workgroup, through mainl_kernel's exchange."""
+    print("case clustered large", flush=True)
+    B, d, F, k = 512, 128, 131072, 128
+    X, W, b = make_inputs(B, d, F, torch.bfloat16, seed=14, device=cuda_dev)
+    b = b.clone()
+    b[70000:70000 + 2 * k] += 50.0
+    _check(X, W, b, k, "bf16", "clustered large")
