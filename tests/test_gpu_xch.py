@@ -169,3 +169,23 @@ def test_best_latents_in_one_w_range_large_batch(cuda_dev):
     b = b.clone()
     b[70000:70000 + 2 * k] += 50.0
     _check(X, W, b, k, "bf16", "clustered large")
+
+
+@pytest.mark.parametrize("B,d,F,k,dtype_name", [
+    (128, 256, 65536, 64, "bf16"),
+    (600, 128, 40000, 64, "bf16"),
+    (1024, 128, 65536, 128, "fp16"),
+])
+def test_sample_pass_path(cuda_dev, monkeypatch, B, d, F, k, dtype_name):
+    """The sample and threshold passes (the path of grids too small for the
+    exchange), forced with STK_TEST_NO_XCH=1 at shapes that would exchange:
+    both paths exact against the oracle (the sampled latents' scores are
+    summed in another order there, so values may differ in the last bit)."""
+    print(f"case sample path B={B} d={d} F={F} k={k} {dtype_name}", flush=True)
+    X, W, b = make_inputs(B, d, F, DT[dtype_name], seed=15, device=cuda_dev)
+    monkeypatch.setenv("STK_TEST_NO_XCH", "1")
+    n = _launches(lambda: topk_sae_cuda_exact(X, W, b, k))
+    assert n["sample_kernel"] == 1 and n["thr_kernel"] == 1, n
+    _check(X, W, b, k, dtype_name, "sample pass")
+    monkeypatch.delenv("STK_TEST_NO_XCH")
+    _check(X, W, b, k, dtype_name, "exchange")
