@@ -224,24 +224,41 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
         p.nwg = (int)cdiv(p.num_tiles, p.tpw);
     }
 
-    // Without a large batch, the first tile of every workgroup seeds the
-    // thresholds (each row's k-th largest of the workgroups' maxima) when
-    // there are enough workgroups for a k-th; otherwise a sample pass does.
-    // (STK_TEST_NO_XCH, a test hook read at each call, selects the sample pass).
-    // Large batches exchange kLXchPerWg maxima per row and workgroup (nwg = the
-    // W ranges per row block), up to 512 per row.
-    if (p.large)
-        p.xch = (int64_t)p.nwg * kLXchPerWg >= k && p.nwg * kLXchPerWg <= 512;
-    else
-        p.xch = p.nwg >= kXchMinWg && p.nwg >= k && p.nwg <= 256;
-    if (std::getenv("STK_TEST_NO_XCH")) p.xch = false;
+    // The thresholds come from the streaming kernel's own first tiles (each
+    // row's k-th largest of the n maxima its workgroups publish, each over m
+    // latents: n = nwg, m = 256 below 512 rows; n = kLXchPerWg * W ranges,
+    // m = 64 above) or from a sample pass of nsamp latents (whose k-th is the
+    // threshold).  A latent passes the exchange's threshold with probability
+    // about -ln(1 - k / n) / m and the sample's about k / nsamp.  The exchange
+    // is taken when it passes at most as many (up to twice as many below 512
+    // rows, where it also saves the two launches of the sample and threshold
+    // passes, a larger share of the call); it needs n > k (n = k is the
+    // minimum of all maxima) and, below 512 rows, at least kXchMinWg
+    // workgroups.  Measured (B = 512-2048, d = 2048-4096, k = 64-128): the
+    // exchange was 3-8 % faster where it passes fewer latents, 1-4 % slower
+    // where it passes ~1.4x as many, and up to 2x slower at n = k.
+    // (STK_TEST_NO_XCH, a test hook read at each call, selects the sample pass.)
+    const int samp_n = (p.large && F >= kSampleLargeMinF) ? kSampleLarge : kSampleTarget;
+    {
+        const int64_t n = p.large ? (int64_t)p.nwg * kLXchPerWg : p.nwg;
+        const double m = p.large ? 64.0 : 256.0;
+        // n = k still bounds the k-th score; without a sample pass (small F)
+        // that weak bound beats none
+        bool ok = (F < kSampleMinF ? n >= k : n > k) && (p.large ? n <= 512 : (p.nwg >= kXchMinWg && p.nwg <= 256));
+        if (ok && F >= kSampleMinF) {
+            const double px = -std::log1p(-(double)k / (double)n) / m;
+            const double ps = (double)k / (double)samp_n;
+            ok = px <= (p.large ? 1.0 : 2.0) * ps;
+        }
+        p.xch = ok && !std::getenv("STK_TEST_NO_XCH");
+    }
     p.sample = F >= kSampleMinF && !p.xch;
     p.samp_log2 = 0;
     p.nsamp = 0;
     if (p.sample) {
         // large batches take a twice larger sample: a tighter threshold halves
         // the candidates their (compute-bound) epilogue and merge handle
-        p.nsamp = (p.large && F >= kSampleLargeMinF) ? kSampleLarge : kSampleTarget;
+        p.nsamp = samp_n;
         p.samp_log2 = ilog2_floor(F / (p.nsamp / kSampleBlock));
     }
     // large batches score the sample with mainl_kernel's sample mode: one
