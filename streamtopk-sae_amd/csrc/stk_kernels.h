@@ -96,12 +96,13 @@ struct MainArgs {
 // least this many workgroups (an owner workgroup handles its rows one wave
 // each: at most 128 / kXchMinWg <= kMainWaves rows).
 constexpr int kXchMinWg = 16;
-// 2 ms at the 100 MHz s_memrealtime clock: far above the skew of the first
-// tile's end over the grid (microseconds), so reached only if some
-// workgroups were not resident.  The exchange's words are read only after
+// 500 us at the 100 MHz s_memrealtime clock: ~30x the longest wait measured
+// (the skew of the first tile's end over the grid plus two round trips,
+// under 15 us), so reached only if some workgroups were not resident (another
+// kernel holding CUs).  The exchange's words are read only after
 // their tag matches the call's; a workspace must therefore be zero-filled
 // before its first use (tag 0 is never a call's).
-constexpr int64_t kXchWaitTicks = 200000;
+constexpr int64_t kXchWaitTicks = 50000;
 
 // Row r's head count is list_cnt[r * kCntStride]: one 128-byte line per row.
 constexpr int kCntStride = 32;
