@@ -240,11 +240,16 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
     // (STK_TEST_NO_XCH, a test hook read at each call, selects the sample pass.)
     const int samp_n = (p.large && F >= kSampleLargeMinF) ? kSampleLarge : kSampleTarget;
     {
-        const int64_t n = p.large ? (int64_t)p.nwg * kLXchPerWg : p.nwg;
+        // mainl_kernel: the W ranges that hold tiles (main_kernel has no empty workgroup)
+        const int64_t nfull = p.large ? cdiv(p.num_tiles, p.tpw) : p.nwg;
+        const int64_t n = p.large ? nfull * kLXchPerWg : p.nwg;
         const double m = p.large ? 64.0 : 256.0;
         // n = k still bounds the k-th score; without a sample pass (small F)
-        // that weak bound beats none
-        bool ok = (F < kSampleMinF ? n >= k : n > k) && (p.large ? n <= 512 : (p.nwg >= kXchMinWg && p.nwg <= 256));
+        // that weak bound beats none.  Only workgroups with a first tile take
+        // part (mainl_kernel's W ranges past the last tile are empty when F is
+        // small); they publish the maxima and own the rows.
+        bool ok = (F < kSampleMinF ? n >= k : n > k) &&
+                  (p.large ? n <= 512 : (p.nwg >= kXchMinWg && p.nwg <= 256));
         if (ok && F >= kSampleMinF) {
             const double px = -std::log1p(-(double)k / (double)n) / m;
             const double ps = (double)k / (double)samp_n;
@@ -344,7 +349,7 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
     if (p.xch) {
         // [nbc][bt][words per row]
         const size_t bt = p.large ? (size_t)kLargeRows : 32 * (size_t)p.NB;
-        const size_t per_row = p.large ? (size_t)p.nwg * kLXchPerWg : (size_t)p.nwg;
+        const size_t per_row = p.large ? (size_t)cdiv(p.num_tiles, p.tpw) * kLXchPerWg : (size_t)p.nwg;
         p.off_xmax = off;
         off = align256(off + (size_t)p.nbc * bt * per_row * 8);
         p.off_xthr = off;
@@ -410,6 +415,7 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     int32_t* list_cnt = (int32_t*)(ws + p.off_lcnt);
     int32_t* seg_cnt = (int32_t*)(ws + p.off_seg);
     uint64_t* err = (uint64_t*)(list_cnt + B * kCntStride);
+    uint32_t* xto = (uint32_t*)(err + 1);   // the exchange's count of polls that ran out
     const uint64_t nonce = next_nonce();
     // STK_TEST_MAX_ROUNDS: the test hook that lowers the retry bounds;
     // STK_TEST_XCH_WAIT: the exchange's wait in ticks (0: every wait runs out
@@ -485,9 +491,11 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         ml.err = err;
         ml.nonce = nonce;
         ml.xch = p.xch ? 1 : 0;
+        ml.xnr = (int)cdiv(p.num_tiles, p.tpw);
         ml.xmax = (uint64_t*)(ws + p.off_xmax);
         ml.xthr = (uint64_t*)(ws + p.off_xthr);
         ml.xwait = xwait;
+        ml.xto = xto;
         int pm = prof_begin("main_kernel", st);
         e = launch_mainl(dt, ml, (int)(p.nbc * p.nwg), st);
         prof_end(pm, st);
@@ -515,6 +523,7 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         ma.xmax = (uint64_t*)(ws + p.off_xmax);
         ma.xthr = (uint64_t*)(ws + p.off_xthr);
         ma.xwait = xwait;
+        ma.xto = xto;
         int pm = prof_begin("main_kernel", st);
         e = launch_main(dt, p.NB, ma, dim3((unsigned)p.nwg, (unsigned)p.nbc), st);
         prof_end(pm, st);

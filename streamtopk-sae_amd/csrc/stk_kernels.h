@@ -90,6 +90,8 @@ struct MainArgs {
     uint64_t* xthr;              // [nbc][32*NB] row thresholds (owner x: rows x, x + gridDim.x, ...)
     int64_t xwait;               // s_memrealtime ticks a wave polls for words before going
                                  //   on without the exchanged thresholds (threshold 0)
+    uint32_t* xto;               // incremented by every poll that runs out with xwait > 0
+                                 //   (the word after the error word; never reset)
 };
 
 // Row blocks of main_kernel whose workgroups exchange thresholds need at
@@ -174,9 +176,12 @@ struct MainLArgs {
     // as MainArgs's, with kLXchPerWg maxima per row and workgroup (one per 64
     // latents of the first tile).  Tagged words as MainArgs's.
     int xch;
-    uint64_t* xmax;              // [nbc][kLargeRows][nr * kLXchPerWg]
+    int xnr;                     // W ranges that hold tiles (the first xnr; the rest are empty
+                                 //   when F is small): only they publish and own rows
+    uint64_t* xmax;              // [nbc][kLargeRows][xnr * kLXchPerWg]
     uint64_t* xthr;              // [nbc][kLargeRows]
     int64_t xwait;
+    uint32_t* xto;
     // sample mode (mainl_sample_kernel): 256-latent tiles of the sampled
     // latents, d split in ksplit ranges; raw partial scores to P
     int ksplit, nsamp;

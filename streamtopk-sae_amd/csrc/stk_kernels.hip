@@ -202,6 +202,8 @@ __device__ __forceinline__ void xch_thresholds(const MainArgs& a, const f32x16 (
         const int quorum = (3 * nwg + 3) / 4;
         if (xch_poll<4>(xmax + (int64_t)row * nwg, nwg, a.k > quorum ? a.k : quorum, tag, a.xwait, lane, v))
             T = xch_kth<4>(v, a.k);
+        else if (lane == 0 && a.xwait > 0)
+            atomicAdd(a.xto, 1u);
         if (lane == 0) xch_put(xthr + row, tag, T);
     }
 
@@ -211,6 +213,7 @@ __device__ __forceinline__ void xch_thresholds(const MainArgs& a, const f32x16 (
         const int base = 64 * wave;
         const int n = nrows - base < 64 ? nrows - base : 64;
         const bool ok = n > 0 && xch_poll<4>(xthr + base, n, n, tag, a.xwait, lane, v);
+        if (n > 0 && !ok && lane == 0 && a.xwait > 0) atomicAdd(a.xto, 1u);
         if (base + lane < BT) thr[base + lane] = xch_key(ok ? v[0] : 0u);
     }
     __syncthreads();

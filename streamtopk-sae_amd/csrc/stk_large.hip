@@ -509,7 +509,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                 // ---- threshold exchange after the first tile (MainArgs::xch's,
                 // with kLXchPerWg maxima per row and workgroup) ----
                 const uint32_t tag = (uint32_t)a.nonce;
-                const int nw = a.nr * kLXchPerWg;   // maxima per row, <= 512 (host)
+                const int nw = a.xnr * kLXchPerWg;  // maxima per row, <= 512 (host)
                 const int nrows = (int)(B - b0 < kLargeRows ? B - b0 : kLargeRows);
                 // the row block passes through an empty asm so that no address
                 // derived from it is hoisted out of the tile loop
@@ -541,17 +541,20 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                             xch_put(xmax + (int64_t)row * nw + rg * kLXchPerWg + (wave & 1) * 2 + q, tag, o);
                     }
                 });
-                // 2. owned rows rg, rg + nr, ...: the k-th largest of the
-                //    row's maxima once max(k, 3/4 nw) have arrived
+                // 2. owned rows rg, rg + xnr, ...: the k-th largest of the
+                //    row's maxima once max(k, 3/4 nw) have arrived (this
+                //    workgroup has tiles, so rg < xnr)
                 const int quorum = (3 * nw + 3) / 4;
                 const int need = a.k > quorum ? a.k : quorum;
                 for (int j = wave;; j += kLWaves) {
-                    const int row = rg + j * a.nr;
+                    const int row = rg + j * a.xnr;
                     if (row >= nrows) break;
                     uint32_t v[8];
                     uint32_t T = 0;
                     if (xch_poll<8>(xmax + (int64_t)row * nw, nw, need, tag, a.xwait, lane, v))
                         T = xch_kth<8>(v, a.k);
+                    else if (lane == 0 && a.xwait > 0)
+                        atomicAdd(a.xto, 1u);
                     if (lane == 0) xch_put(xthr + row, tag, T);
                 }
                 // 3. wave w reads rows 64 w .. 64 w + 63
@@ -560,6 +563,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                     const int base = 64 * wave;
                     const int n = nrows - base < 64 ? nrows - base : 64;
                     const bool ok = n > 0 && xch_poll<1>(xthr + base, n, n, tag, a.xwait, lane, v);
+                    if (n > 0 && !ok && lane == 0 && a.xwait > 0) atomicAdd(a.xto, 1u);
                     thr[base + lane] = xch_key(ok ? v[0] : 0u);
                 }
                 __syncthreads();

@@ -69,6 +69,7 @@ def _launches(fn):
     (40, 16384 + 37, 128, False),  # 65 workgroups < k: the sample pass seeds the thresholds
     (600, 65536, 64, True),      # large batch: mainl_kernel, 80 W ranges x 4 maxima per row
     (4096, 65536, 128, False),   # 16 W ranges x 4 maxima < k: mainl_kernel with a sample pass
+    (512, 20000, 64, True),      # 79 tiles over 128 W ranges: the 79 that hold tiles exchange
 ])
 def test_exchange_replaces_threshold_passes(cuda_dev, B, F, k, xch):
     print(f"case launches B={B} F={F} k={k}", flush=True)
@@ -88,6 +89,7 @@ def test_exchange_replaces_threshold_passes(cuda_dev, B, F, k, xch):
     (300, 96, 30000, 32, "fp32"),   # three row blocks, each its own exchange
     (600, 128, 30000, 64, "bf16"),  # mainl_kernel, three row blocks
     (1024, 256, 65536, 128, "fp16"),
+    (512, 64, 20000, 32, "bf16"),   # mainl_kernel with empty W ranges
 ])
 def test_exchange_waits_run_out(cuda_dev, monkeypatch, B, d, F, k, dtype_name):
     """Every exchange wait runs out at once: thresholds stay 0 and the result is still exact."""
@@ -189,3 +191,43 @@ def test_sample_pass_path(cuda_dev, monkeypatch, B, d, F, k, dtype_name):
     _check(X, W, b, k, dtype_name, "sample pass")
     monkeypatch.delenv("STK_TEST_NO_XCH")
     _check(X, W, b, k, dtype_name, "exchange")
+
+
+def _timeouts(X):
+    """The exchange's count of polls that ran out, in the workspace the op
+    keeps for X's device and current stream: the 32-bit word after the error
+    word (workspace offset align256(8 B) + 128 B + 8)."""
+    from streamtopk_sae import ops
+    B = X.shape[0]
+    key = (X.device.index, int(torch.cuda.current_stream(X.device).cuda_stream))
+    torch.cuda.synchronize()
+    ws = ops._WS[key]
+    off = ((B * 8 + 255) // 256) * 256 + B * 128 + 8
+    return int(ws[off:off + 4].cpu().view(torch.int32)[0])
+
+
+@pytest.mark.parametrize("B,d,F,k,short_waits", [
+    (128, 768, 65536, 32, True),      # config 1's shape
+    (128, 2048, 262144, 64, False),   # config 2's shape
+    (40, 256, 16384 + 37, 64, True),
+    (300, 128, 100000, 64, False),
+    (600, 128, 65536, 64, True),      # mainl_kernel
+    (1024, 256, 262144, 128, False),  # mainl_kernel, config 4's grid
+    (512, 64, 20000, 64, True),       # mainl_kernel, 79 of 128 W ranges hold tiles
+])
+def test_exchange_never_runs_out(cuda_dev, monkeypatch, B, d, F, k, short_waits):
+    """On an idle device every workgroup of the grid is resident, so no poll of
+    the exchange runs out (one that did would leave thresholds at 0: exact but
+    slow).  At the smaller shapes a wait of 1 tick makes them run out, which
+    the count shows (the larger ones would take long with threshold 0)."""
+    print(f"case xch no timeout B={B} d={d} F={F} k={k}", flush=True)
+    X, W, b = make_inputs(B, d, F, torch.bfloat16, seed=16, device=cuda_dev)
+    topk_sae_cuda_exact(X, W, b, k)   # sizes the op's workspace
+    before = _timeouts(X)
+    for _ in range(5):
+        topk_sae_cuda_exact(X, W, b, k)
+    assert _timeouts(X) == before
+    if short_waits:
+        monkeypatch.setenv("STK_TEST_XCH_WAIT", "1")
+        _check(X, W, b, k, "bf16", "1-tick waits")
+        assert _timeouts(X) > before
