@@ -72,8 +72,8 @@ struct MainArgs {
     int sampled;                 // non-zero: the sampled latents (is_sampled) were
     int samp_log2, samp_blocks;  //   scored by the sample pass and are skipped here
     uint64_t* list_keys;         // [B][list_cap]: row r's head (head_span slots, the
-    int64_t list_cap, head_span; //   sample's top k), then one segment of cap keys
-                                 //   per workgroup (gridDim.x of them)
+    int64_t list_cap, head_span; //   sample's top k; none with the exchange), then one
+                                 //   segment of cap keys per workgroup (gridDim.x of them)
     int32_t* seg_cnt;            // [B][gridDim.x] keys each workgroup left in its segment
     int lq;                      // LDS queue keys per row (even, <= 64; cap >= k + lq)
     int max_rounds;              // bound of the epilogue's spill-and-retry loop

@@ -1,20 +1,24 @@
 // stk_kernels.hip -- the exact streaming top-k encoder on gfx950.
 //
+//   main_kernel    : streams W once; MFMA scores for 256 latents x up to 128
+//                    rows per tile; scores not below the row threshold go to
+//                    a short per-row LDS queue, which spills to the
+//                    workgroup's segment of the row's list when it fills; a
+//                    full segment is rank-compacted to its top-k.  At the end
+//                    every queue is flushed to its segment.  The row
+//                    thresholds come from the workgroups' first tiles
+//                    (xch_thresholds: each row's k-th largest of the
+//                    workgroups' maxima), or, for grids too small for that,
+//                    from the two passes below (then the sampled latents are
+//                    skipped here: each latent is scored by exactly one kernel).
 //   sample_kernel  : fp32 partial sums (one per d range) of the scores of the
 //                    sampled latents (blocks of 128 consecutive latents spread
 //                    over F) for every row.
 //   thr_kernel     : per row, the k-th largest sampled key: a lower bound of
 //                    the row's k-th key; the sample's top k open the row's
 //                    candidate list.
-//   main_kernel    : streams W once; MFMA scores for 256 latents x up to 128
-//                    rows per tile (the sampled latents are skipped: each latent
-//                    is scored by exactly one kernel); scores not below the
-//                    row threshold go to a short per-row LDS queue, which
-//                    spills to the workgroup's segment of the row's list when
-//                    it fills; a full segment is rank-compacted to its top-k.
-//                    At the end every queue is flushed to its segment.
 //   merge_seg_kernel / merge_kernel : per row, top-k of its candidate list
-//                    (the head and one segment per workgroup).
+//                    (the head, if any, and one segment per workgroup).
 //
 // The reference's pass 1 / pass 2 split (streamtopk_exact.cu:58-187 tile
 // kernel, :429-499 merge kernel) maps to main_kernel / merge_kernel; its

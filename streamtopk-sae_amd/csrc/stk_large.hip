@@ -28,10 +28,14 @@
 //   - grid: workgroups are placed so that the row blocks sharing a W range
 //     run on one XCD (workgroup i runs on XCD i % 8), and W is fetched into
 //     that XCD's L2 once for all of them.
+//   - row thresholds: after the first tile every workgroup publishes the
+//     largest score of each 64-latent quarter of it per row, and each row's
+//     owner takes the k-th largest of those maxima (the threshold exchange,
+//     as main_kernel's; MainLArgs::xch).
 // mainl_kernel<DT, true> (sample mode) computes the raw scores of the
-// sampled latents with the same machinery: one 256-latent tile of them per
-// workgroup and a d range per workgroup, partial sums summed in a fixed order
-// by thr_kernel.
+// sampled latents with the same machinery, for grids too small for the
+// exchange: one 256-latent tile of them per workgroup and a d range per
+// workgroup, partial sums summed in a fixed order by thr_kernel.
 // The reference has no counterpart: its B >= #SMs path streams all of W per
 // row (streamtopk_exact.cu:506-638).
 #include "stk_kernels.h"
