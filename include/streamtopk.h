@@ -117,7 +117,8 @@ int stk_topk_merge(const float* Vp, const int32_t* Ip, int64_t nparts, int64_t B
                    float* V, int32_t* I, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Device workspace (bytes) for stk_approx_forward.  `with_candidates` is
- * non-zero when the caller passes a candidate buffer. */
+ * non-zero when the caller passes a candidate buffer (then the workspace holds
+ * each group's first candidate as an 8-byte key: B * ceil(F/128) * 8 bytes). */
 int stk_approx_workspace_bytes(int64_t B, int64_t d, int64_t F, int64_t k, int64_t c, int dtype,
                                int with_candidates, size_t* out_bytes);
 

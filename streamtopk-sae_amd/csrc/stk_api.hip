@@ -795,7 +795,9 @@ int stk_approx_workspace_bytes(int64_t B, int64_t d, int64_t F, int64_t k, int64
     if (!out_bytes) return set_error(STK_E_INVALID, "null out_bytes");
     int rc = validate_approx(B, d, F, k, c, dtype);
     if (rc) return rc;
-    if (with_candidates || B == 0) { *out_bytes = 0; return 0; }
+    if (B == 0) { *out_bytes = 0; return 0; }
+    // with a candidate buffer: the groups' head keys, B x ceil(F / 128) words
+    if (with_candidates) { *out_bytes = align256((size_t)B * cdiv(F, kApproxGroup) * 8); return 0; }
     int ncu = 0;
     if ((rc = cu_count(&ncu))) return rc;
     *out_bytes = make_exact_plan(B, d, F, k, dtype, ncu).total;
@@ -834,16 +836,23 @@ int stk_approx_forward(const void* X, const void* W, const float* b, float* V, i
         return run_exact(p, X, W, b, V, I, B, d, F, k, dtype, (unsigned char*)workspace, st);
     }
     const GroupPlan p = make_group_plan(B, F, ncu);
+    const size_t heads_bytes = (size_t)B * p.num_groups * 8;
+    if (!workspace || workspace_bytes < heads_bytes)
+        return set_error(STK_E_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required",
+                         workspace ? workspace_bytes : (size_t)0, heads_bytes);
+    if ((uintptr_t)workspace & 255) return set_error(STK_E_INVALID, "workspace must be 256-byte aligned");
     GroupArgs ga;
     ga.X = X; ga.W = W; ga.bias = b; ga.B = B; ga.d = d; ga.F = F; ga.c = (int)c;
     ga.num_groups = p.num_groups; ga.tiles_per_wg = p.tpw;
     ga.cand_vals = cand_vals; ga.cand_idxs = cand_idxs;
+    ga.heads = (uint64_t*)workspace;
     int pg = prof_begin("group_kernel", st);
     hipError_t e = launch_group(dtype, p.NB, ga, dim3((unsigned)p.nwg, (unsigned)p.nbc), st);
     prof_end(pg, st);
     if (e != hipSuccess) return hip_fail(e, "group_kernel launch");
     CandArgs ca;
     ca.cand_vals = cand_vals; ca.cand_idxs = cand_idxs;
+    ca.heads = (const uint64_t*)workspace;
     ca.num_groups = p.num_groups; ca.c = (int)c; ca.k = (int)k; ca.V = V; ca.I = I;
     pg = prof_begin("cand_kernel", st);
     e = launch_cand(ca, B, st);

@@ -262,6 +262,9 @@ __device__ __forceinline__ void sort_segment(const GroupArgs& a, const uint32_t*
         *(f32x4*)(a.cand_vals + o + 4) = f32x4{val[4], val[5], val[6], val[7]};
         *(u32x4*)(a.cand_idxs + o) = u32x4{idx[0], idx[1], idx[2], idx[3]};
         *(u32x4*)(a.cand_idxs + o + 4) = u32x4{idx[4], idx[5], idx[6], idx[7]};
+        // the group's head (entry 0, this lane's first) as cand_kernel keys it
+        if (l == 0)
+            a.heads[(rowblk + rlv) * G + grp] = idx[0] != 0xFFFFFFFFu ? make_key(val[0], (int32_t)idx[0]) : 0ull;
     }
 }
 
@@ -335,12 +338,12 @@ __global__ __launch_bounds__(kMainThreads, 1) void group_kernel(GroupArgs a)
 }
 
 // Key of group g's head (its largest candidate), 0 for a padded group.
-__device__ __forceinline__ uint64_t head_key(const float* cv, const int32_t* ci, int64_t g, int64_t G, int c)
+// Group g's head key from the compact heads (0 past the last group): one
+// 8-byte word per group instead of a value and an index c entries apart.
+__device__ __forceinline__ uint64_t head_key(const uint64_t* hd, int64_t g, int64_t G)
 {
-    const int64_t gg = g < G ? g : G - 1;
-    const int32_t idx = ci[gg * c];
-    const float val = cv[gg * c];
-    return (g < G && idx >= 0) ? make_key(val, idx) : 0ull;
+    const uint64_t h = hd[g < G ? g : G - 1];
+    return g < G ? h : 0ull;
 }
 
 // Per row: top-k over the (value, index) candidates of every group.  Each
@@ -358,12 +361,13 @@ __global__ __launch_bounds__(kThreads) void cand_kernel(CandArgs a)
     const int64_t G = a.num_groups;
     const float* cv = a.cand_vals + row * G * c;
     const int32_t* ci = a.cand_idxs + row * G * c;
+    const uint64_t* hd = a.heads + row * G;
 
     uint64_t m = 0;
     for (int64_t g0 = tid; g0 < G; g0 += U * kThreads) {
         uint64_t hk[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) hk[u] = head_key(cv, ci, g0 + u * kThreads, G, c);
+        for (int u = 0; u < U; ++u) hk[u] = head_key(hd, g0 + u * kThreads, G);
 #pragma unroll
         for (int u = 0; u < U; ++u) m = hk[u] > m ? hk[u] : m;
     }
@@ -380,7 +384,7 @@ __global__ __launch_bounds__(kThreads) void cand_kernel(CandArgs a)
         for (; g0 < G; g0 += U * kThreads, u0 = 0, e0 = 0) {
             uint64_t hk[U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) hk[u] = head_key(cv, ci, g0 + u * kThreads, G, c);
+            for (int u = 0; u < U; ++u) hk[u] = head_key(hd, g0 + u * kThreads, G);
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 if (stalled || u < u0 || hk[u] <= thr) continue;

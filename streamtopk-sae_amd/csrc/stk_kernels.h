@@ -235,11 +235,13 @@ struct GroupArgs {               // approximate variant, per-group top-c candida
     int64_t num_groups, tiles_per_wg;
     float* cand_vals;            // [B][num_groups][c]
     int32_t* cand_idxs;          // [B][num_groups][c]
+    uint64_t* heads;             // [B][num_groups] each group's first candidate as a key (0: none)
 };
 
 struct CandArgs {                // approximate variant, top-k over the candidates
     const float* cand_vals;
     const int32_t* cand_idxs;
+    const uint64_t* heads;       // [B][num_groups] as GroupArgs::heads
     int64_t num_groups;          // candidates per row: num_groups * c, each group's in descending order
     int c, k;
     float* V;
