@@ -19,10 +19,13 @@
  *     for the legacy default stream) on the current HIP device; all pointers
  *     must be device pointers on that device, 16-byte aligned.
  *   - A workspace must be zero-filled before its first use (hipMemset once,
- *     when it is allocated); every call leaves it valid for the next call of
- *     any shape.  Calls that overlap in time must not share a workspace.
- *     (The exact path's workgroups exchange per-row thresholds through words
- *     tagged with the call's number; zero is never a call's tag.)
+ *     when it is allocated), and again after a call on it returned an error;
+ *     every successful call leaves it valid for the next call of any shape,
+ *     also when the calls are replays of a captured HIP graph.  Calls that
+ *     overlap in time must not share a workspace.  (The exact path's
+ *     workgroups exchange per-row thresholds through words tagged with the
+ *     call's number, kept in the workspace's first 256 bytes and advanced by
+ *     each call on the device; zero is never a call's tag.)
  */
 #ifndef STREAMTOPK_H
 #define STREAMTOPK_H

@@ -2,10 +2,6 @@
 // reference's error wording, launch planning for the current device, and the
 // kernel sequence of each entry point.  No device memory is allocated here:
 // every temporary lives in the caller's workspace.
-#include <unistd.h>
-
-#include <atomic>
-#include <chrono>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -160,26 +156,6 @@ static int ilog2_floor(int64_t x) { int l = 0; while ((x >> (l + 1)) > 0) ++l; r
 // ---------------------------------------------------------------------------
 // Exact-path plan
 // ---------------------------------------------------------------------------
-// The tag of one call's kernels (MainArgs::nonce): distinct for every call
-// of the process, and its low 32 bits (the exchange's word tag) are never 0
-// and differ between consecutive calls.  The sequence starts at a value drawn
-// from the clock, the process id and an address.
-static uint64_t next_nonce()
-{
-    static std::atomic<uint64_t> ctr{[] {
-        uint64_t z = (uint64_t)std::chrono::steady_clock::now().time_since_epoch().count();
-        z ^= (uint64_t)getpid() << 32;
-        z ^= (uint64_t)(uintptr_t)&g_err;
-        // splitmix64 finaliser
-        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-        return z ^ (z >> 31);
-    }()};
-    uint64_t n;
-    do { n = ctr.fetch_add(1, std::memory_order_relaxed) + 1; } while ((uint32_t)n == 0);
-    return n;
-}
-
 struct ExactPlan {
     bool large;                  // mainl_kernel (B >= kLargeMinB) instead of main_kernel
     bool xch;                    // main_kernel exchanges thresholds after its first tile (no sample pass)
@@ -336,11 +312,11 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
     const int64_t p_keys = p.sample ? ((int64_t)p.ksplit * p.nsamp + 1) / 2 : 0;
     if (p_keys > seg_keys) seg_keys = p_keys;
     p.list_cap = (p.head_span + seg_keys + 1) & ~(int64_t)1;
-    size_t off = 0;
+    size_t off = kCtlBytes;   // the control line (epoch, timeouts, error word, tag) at 0
     p.off_thr = off;
     off = align256(off + (size_t)B * 8);
     p.off_lcnt = off;
-    off = align256(off + (size_t)B * 4 * kCntStride + 4 * kCntStride);   // + the error word's line
+    off = align256(off + (size_t)B * 4 * kCntStride);
     p.off_seg = off;
     off = align256(off + (size_t)B * p.nwg * 4);
     p.off_list = off;
@@ -414,9 +390,11 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     uint64_t* list_keys = (uint64_t*)(ws + p.off_list);
     int32_t* list_cnt = (int32_t*)(ws + p.off_lcnt);
     int32_t* seg_cnt = (int32_t*)(ws + p.off_seg);
-    uint64_t* err = (uint64_t*)(list_cnt + B * kCntStride);
-    uint32_t* xto = (uint32_t*)(err + 1);   // the exchange's count of polls that ran out
-    const uint64_t nonce = next_nonce();
+    // the control line: epoch (u32), poll timeouts (u32), error word, call tag
+    uint32_t* epoch = (uint32_t*)ws;
+    uint32_t* xto = epoch + 1;
+    uint64_t* err = (uint64_t*)(ws + 8);
+    uint64_t* cur = (uint64_t*)(ws + 16);
     // STK_TEST_MAX_ROUNDS: the test hook that lowers the retry bounds;
     // STK_TEST_XCH_WAIT: the exchange's wait in ticks (0: every wait runs out
     // at once, the path of workgroups that were never resident)
@@ -489,7 +467,8 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         ml.seg_cnt = seg_cnt;
         ml.max_rounds = max_rounds >= 0 ? max_rounds : kMainLMaxRounds;
         ml.err = err;
-        ml.nonce = nonce;
+        ml.epoch = epoch;
+        ml.cur = cur;
         ml.xch = p.xch ? 1 : 0;
         ml.xnr = (int)cdiv(p.num_tiles, p.tpw);
         ml.xmax = (uint64_t*)(ws + p.off_xmax);
@@ -518,7 +497,8 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         ma.lq = p.lq;
         ma.max_rounds = max_rounds >= 0 ? max_rounds : kMainMaxRounds;
         ma.err = err;
-        ma.nonce = nonce;
+        ma.epoch = epoch;
+        ma.cur = cur;
         ma.xch = p.xch ? 1 : 0;
         ma.xmax = (uint64_t*)(ws + p.off_xmax);
         ma.xthr = (uint64_t*)(ws + p.off_xthr);
@@ -540,7 +520,8 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     mg.k = (int)k;
     mg.f_offset = (int32_t)f_offset;
     mg.err = err;
-    mg.nonce = nonce;
+    mg.cur = cur;
+    mg.epoch = epoch;
     mg.ties = 0;   // one encode's keys are distinct
     mg.V = V; mg.I = I;
     const int pg = prof_begin("merge_kernel", st);
@@ -601,8 +582,9 @@ static int validate_approx(int64_t B, int64_t d, int64_t F, int64_t k, int64_t c
 // at zero: every count and key a kernel reads is written earlier in the same
 // call (thr_kernel or the exchange each row's threshold, thr_kernel the head
 // counts, main_kernel every segment count), and the words compared with the
-// call's nonce (the exchange's flags, the error word) never hold it before
-// the call writes them.
+// call's tag (the exchange's words, the error word) never hold it before the
+// call writes them: the tag is the epoch of the control line + 1, zero at
+// load, advanced by every call.
 __attribute__((used)) static __device__ __align__(256) unsigned char scratch[STK_NOALLOC_SCRATCH_BYTES];
 
 static std::mutex g_scratch_mu;

@@ -76,8 +76,8 @@ __device__ __forceinline__ uint64_t make_key(float v, int64_t idx)
 
 // ---------------------------------------------------------------------------
 // Threshold exchange helpers (main_kernel, mainl_kernel).  Every word the
-// workgroups of one call share carries the call's tag (the low 32 bits of its
-// nonce, never 0) in its high half and its data in the low half, and is
+// workgroups of one call share carries the call's tag (the workspace's epoch
+// + 1, never 0) in its high half and its data in the low half, and is
 // written and read whole with agent-scope atomic stores and loads (coherent
 // across the XCDs' L2s word by word).  A reader polls the words it needs
 // until enough carry the call's tag: no flag has to be ordered after the

@@ -77,14 +77,15 @@ struct MainArgs {
     int32_t* seg_cnt;            // [B][gridDim.x] keys each workgroup left in its segment
     int lq;                      // LDS queue keys per row (even, <= 64; cap >= k + lq)
     int max_rounds;              // bound of the epilogue's spill-and-retry loop
-    uint64_t* err;               // set to `nonce` if that bound is ever reached
-    uint64_t nonce;              // this call's tag (non-zero, unique per call in the process)
+    uint64_t* err;               // set to the call's tag if that bound is ever reached
+    const uint32_t* epoch;       // the workspace's call count: this call's tag is *epoch + 1
+    uint64_t* cur;               // receives the call's tag (for the merge's error check)
     // Threshold exchange (xch != 0; then thr0 is null and nothing is sampled):
     // after its first tile every workgroup publishes each row's largest score
     // of that tile, the owner of a row takes the k-th largest of those maxima
     // as the row's threshold, and every workgroup reads its rows' thresholds
     // before its first epilogue filters anything.  Each word: the call's tag
-    // (low 32 bits of nonce) << 32 | a score image (ordered_u32).
+    // tag << 32 | a score image (ordered_u32).
     int xch;
     uint64_t* xmax;              // [nbc][32*NB][gridDim.x] each workgroup's row maxima
     uint64_t* xthr;              // [nbc][32*NB] row thresholds (owner x: rows x, x + gridDim.x, ...)
@@ -98,6 +99,16 @@ struct MainArgs {
 // least this many workgroups (an owner workgroup handles its rows one wave
 // each: at most 128 / kXchMinWg <= kMainWaves rows).
 constexpr int kXchMinWg = 16;
+// Every exact-path workspace starts with a control line (kCtlBytes): the
+// epoch (u32 at 0: calls completed on this workspace, advanced by each call's
+// merge), the exchange's count of polls that ran out (u32 at 4), the error
+// word (u64 at 8) and the running call's tag (u64 at 16).  A call's tag is
+// epoch + 1 (epoch wraps below 0xFFFFFFFF, so a tag is never 0): it differs
+// from every earlier call's on the workspace, whatever their shapes, also when
+// the call is a replay of a captured graph (whose kernel arguments never
+// change), so words that earlier calls left carry other tags.
+constexpr size_t kCtlBytes = 256;
+
 // 500 us at the 100 MHz s_memrealtime clock: ~30x the longest wait measured
 // (the skew of the first tile's end over the grid plus two round trips,
 // under 15 us), so reached only if some workgroups were not resident (another
@@ -113,10 +124,10 @@ constexpr int kCntStride = 32;
 // number of rounds.  The bounds are never reached (main_kernel places at least
 // lq >= 8 of a row's <= 256 pending scores per round, mainl_kernel at least
 // cap - k >= 64), so they only guard against a broken invariant: reaching one
-// sets the workspace's error word to the call's nonce, and the merge of that
+// sets the workspace's error word to the call's tag, and the merge of that
 // call then marks every row of its output (indices -1, values NaN) instead of
-// returning a silently wrong result.  A word holding another call's nonce (or
-// anything else) means no error: nothing has to clear it between calls.
+// returning a silently wrong result.  A word holding another call's tag (or
+// zero) means no error: nothing has to clear it between calls.
 // STK_TEST_MAX_ROUNDS=n in the environment allows n spill rounds instead (a
 // test hook that forces that path from the host; 0: none).
 constexpr int kMainMaxRounds = 4096;
@@ -170,8 +181,9 @@ struct MainLArgs {
     int64_t list_cap, head_span;
     int32_t* seg_cnt;            // [B][nr] keys in each segment
     int max_rounds;              // bound of the overflow loop (see kMainLMaxRounds)
-    uint64_t* err;               // set to `nonce` if that bound is ever reached
-    uint64_t nonce;
+    uint64_t* err;               // set to the call's tag if that bound is ever reached
+    const uint32_t* epoch;       // as MainArgs's
+    uint64_t* cur;
     // Threshold exchange (xch != 0; then thr0 is null and nothing is sampled),
     // as MainArgs's, with kLXchPerWg maxima per row and workgroup (one per 64
     // latents of the first tile).  Tagged words as MainArgs's.
@@ -210,8 +222,9 @@ struct MergeArgs {
     int32_t f_offset;            // added to every emitted index (a shard's first latent)
     int ties;                    // non-zero: keys may repeat (stk_topk_merge's parts); equal keys
                                  //   take consecutive ranks
-    const uint64_t* err;         // equal to `nonce`: mark the output rows (-1, NaN); may be null
-    uint64_t nonce;
+    const uint64_t* err;         // equal to *cur (this call's tag): mark the output rows
+    const uint64_t* cur;         //   (-1, NaN); both null for stk_topk_merge
+    uint32_t* epoch;             // advanced by one (workgroup 0), or null
     float* V;
     int32_t* I;
 };

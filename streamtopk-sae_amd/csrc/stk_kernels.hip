@@ -164,14 +164,13 @@ __device__ __forceinline__ void flush_rows(int* cnt, int* gcnt, uint64_t* thr, c
 // epilogue runs.
 template <int NB>
 __device__ __forceinline__ void xch_thresholds(const MainArgs& a, const f32x16 (&ac)[NB], uint32_t vmask,
-                                               uint64_t* thr, uint32_t* scr, int64_t b0, int tid)
+                                               uint64_t* thr, uint32_t* scr, int64_t b0, int tid, uint32_t tag)
 {
     constexpr int BT = 32 * NB;
     const int lane = tid & 63, wave = tid >> 6, h = lane >> 5, jl = lane & 31;
     const int nwg = (int)gridDim.x, x = (int)blockIdx.x;
     const int nrows = (int)(a.B - b0 < BT ? a.B - b0 : BT);
     const int nown = nwg < nrows ? nwg : nrows;
-    const uint32_t tag = (uint32_t)a.nonce;
     // the row block passes through an empty asm so that no address derived
     // from it is hoisted out of the tile loop (kept live, it would spill)
     int64_t yb = blockIdx.y;
@@ -244,6 +243,10 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
     const int64_t b0 = (int64_t)blockIdx.y * BT;
     const int64_t B = a.B, F = a.F;
     const int k = a.k;
+    // this call's tag: the workspace's epoch (advanced by the previous call's
+    // merge) + 1, recorded for this call's merge
+    const uint32_t tag = *a.epoch + 1u;
+    if (tid == 0) *a.cur = tag;
     // this workgroup's global segments: cap keys in each row's list (row
     // b0 + r at seg + r * list_cap; rows past B are never written)
     uint64_t* seg = a.list_keys + b0 * a.list_cap + a.head_span + (int64_t)blockIdx.x * cap;
@@ -292,7 +295,7 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
                 vmask |= ok ? (1u << r) : 0u;
             }
         }
-        if (a.xch && t == 0) xch_thresholds<NB>(a, ac, vmask, thr, (uint32_t*)(smem + TS::kWBuf), b0, tid);
+        if (a.xch && t == 0) xch_thresholds<NB>(a, ac, vmask, thr, (uint32_t*)(smem + TS::kWBuf), b0, tid, tag);
         // ---- scores not below the row threshold ----
         // The float test keeps every score whose key beats the threshold key
         // (and possibly a few equal to its value: harmless extra candidates).
@@ -343,7 +346,7 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
             if (it >= a.max_rounds) {
                 // unreachable by the bound's argument (kMainMaxRounds): the
                 // pending scores are lost, so the call's result is marked
-                if (tid == 0) __hip_atomic_store(a.err, a.nonce, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (tid == 0) __hip_atomic_store(a.err, (uint64_t)tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
             __syncthreads();   // the LDS queues are complete
@@ -690,14 +693,20 @@ __device__ __forceinline__ void merge_pass(SelSharedT<NT>& S, const uint64_t (&v
 // at once, unconditionally (clamped into the row's list, masked afterwards),
 // together with the row's count; every other slot is loaded only if it holds
 // a candidate.
-// Whether the error word holds this call's nonce (a streaming kernel of the
+// Whether the error word holds this call's tag (a streaming kernel of the
 // call lost candidates); if so, row `row` of the output is marked: indices
 // -1, values NaN.  The word is the same for every thread, so the whole
-// workgroup returns together.
+// workgroup returns together.  Workgroup 0 also advances the workspace's
+// epoch for the next call (no other kernel of this call reads it; the
+// streaming kernel has recorded this call's tag in *cur).
 template <int NT = kThreads>
 __device__ __forceinline__ bool merge_marked(const MergeArgs& a, int64_t row, int tid)
 {
-    if (a.err == nullptr || *a.err != a.nonce) return false;
+    if (a.epoch != nullptr && blockIdx.x == 0 && tid == 0) {
+        const uint32_t e = *a.epoch + 1u;
+        *a.epoch = e == 0xFFFFFFFFu ? 0u : e;
+    }
+    if (a.err == nullptr || *a.err != *a.cur) return false;
     for (int r = tid; r < a.k; r += NT) {
         a.V[row * a.k + r] = __builtin_nanf("");
         a.I[row * a.k + r] = -1;

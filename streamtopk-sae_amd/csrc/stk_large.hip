@@ -307,7 +307,11 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
     const int64_t b0 = (int64_t)rb * kLargeRows;
     const int64_t B = a.B, F = a.F;
 
+    // this call's tag (MainArgs::epoch), recorded for this call's merge
+    uint32_t tag = 0;
     if (!SAMPLE) {
+        tag = *a.epoch + 1u;
+        if (blockIdx.x == 0 && tid == 0) *a.cur = tag;
         for (int i = tid; i < kLargeRows; i += kLargeThreads) {
             const int64_t row = b0 + i;
             cnt[i] = 0;
@@ -512,7 +516,6 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
             if (a.xch && t == 0) {
                 // ---- threshold exchange after the first tile (MainArgs::xch's,
                 // with kLXchPerWg maxima per row and workgroup) ----
-                const uint32_t tag = (uint32_t)a.nonce;
                 const int nw = a.xnr * kLXchPerWg;  // maxima per row, <= 512 (host)
                 const int nrows = (int)(B - b0 < kLargeRows ? B - b0 : kLargeRows);
                 // the row block passes through an empty asm so that no address
@@ -596,7 +599,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                         if (it >= a.max_rounds) {
                             // unreachable by the bound's argument (kMainLMaxRounds):
                             // the pending scores are lost, so the result is marked
-                            if (tid == 0) __hip_atomic_store(a.err, a.nonce, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            if (tid == 0) __hip_atomic_store(a.err, (uint64_t)tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                             break;
                         }
                         __threadfence_block();   // this thread's segment stores are complete

@@ -18,7 +18,8 @@ stream) and reused by later calls on that stream, grown when a call needs more:
 calls queued on one stream run one after another, and calls on different
 streams get different workspaces.  A new workspace is zero-filled, as the
 library requires before a workspace's first use; calls leave it valid for the
-next.  ``clear_workspace_cache()`` releases them.
+next, and a call that fails drops it.  ``clear_workspace_cache()`` releases
+them.
 """
 import ctypes
 import threading
@@ -54,6 +55,16 @@ def _workspace(device, stream, nbytes):
             ws = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
             _WS[key] = ws
         return ws
+
+
+def _check_drop(rc, device, stream):
+    """_lib.check, dropping the stream's cached workspace on failure: a call
+    that failed part-way may not have advanced the workspace's epoch, so its
+    words could pass for the next call's; the next call zero-fills a new one."""
+    if rc != 0:
+        with _WS_LOCK:
+            _WS.pop((device.index, int(stream)), None)
+    _lib.check(rc)
 
 
 def clear_workspace_cache():
@@ -195,7 +206,7 @@ def exact_forward(X, W_enc, b_enc, k, f_offset=0):
         else:
             rc = lib.stk_exact_forward(_ptr(X), _ptr(W_enc), _ptr(b_enc), _ptr(V), _ptr(I),
                                        B, d, F, k, dt, _ptr(ws), ws.numel(), ctypes.c_void_p(stream))
-        _lib.check(rc)
+        _check_drop(rc, X.device, stream)
     return V, I
 
 
@@ -290,7 +301,7 @@ def approx_forward(X, W_enc, b_enc, k, c, candidate_buffer=None, candidates=Fals
         rc = lib.stk_approx_forward(_ptr(X), _ptr(W_enc), _ptr(b_enc), _ptr(V), _ptr(I),
                                     B, d, F, k, c, dt, _ptr(cand_vals), _ptr(cand_idxs),
                                     _ptr(ws), ws.numel(), ctypes.c_void_p(stream))
-        _lib.check(rc)
+        _check_drop(rc, X.device, stream)
         if copy_back is not None:
             copy_back.copy_(cand_vals)
             cand_vals = copy_back

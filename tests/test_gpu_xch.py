@@ -195,15 +195,13 @@ def test_sample_pass_path(cuda_dev, monkeypatch, B, d, F, k, dtype_name):
 
 def _timeouts(X):
     """The exchange's count of polls that ran out, in the workspace the op
-    keeps for X's device and current stream: the 32-bit word after the error
-    word (workspace offset align256(8 B) + 128 B + 8)."""
+    keeps for X's device and current stream: the second 32-bit word of the
+    workspace's control line (after the epoch)."""
     from streamtopk_sae import ops
-    B = X.shape[0]
     key = (X.device.index, int(torch.cuda.current_stream(X.device).cuda_stream))
     torch.cuda.synchronize()
     ws = ops._WS[key]
-    off = ((B * 8 + 255) // 256) * 256 + B * 128 + 8
-    return int(ws[off:off + 4].cpu().view(torch.int32)[0])
+    return int(ws[4:8].cpu().view(torch.int32)[0])
 
 
 @pytest.mark.parametrize("B,d,F,k,short_waits", [
@@ -231,3 +229,42 @@ def test_exchange_never_runs_out(cuda_dev, monkeypatch, B, d, F, k, short_waits)
         monkeypatch.setenv("STK_TEST_XCH_WAIT", "1")
         _check(X, W, b, k, "bf16", "1-tick waits")
         assert _timeouts(X) > before
+
+
+@pytest.mark.parametrize("B,d,F,k", [
+    (128, 256, 65536, 32),      # main_kernel's exchange
+    (600, 128, 81920, 64),      # mainl_kernel's
+])
+def test_graph_replays_with_new_inputs(cuda_dev, B, d, F, k):
+    """The op captured in a graph and replayed with new inputs each time.
+    A replay's kernel arguments never change, so the exchange's tag must not
+    come from them: it is the workspace's epoch + 1, advanced by every call's
+    merge.  Each replay is checked against the oracle and against an eager
+    call on the same inputs (bit for bit), with eager work and
+    synchronisations between the replays."""
+    print(f"case graph replay B={B} d={d} F={F} k={k}", flush=True)
+    X, W, b = make_inputs(B, d, F, torch.bfloat16, seed=17, device=cuda_dev)
+    s = torch.cuda.Stream(cuda_dev)
+    s.wait_stream(torch.cuda.current_stream(cuda_dev))
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            topk_sae_cuda_exact(X, W, b, k)   # the op's workspace for s, outside the capture
+    torch.cuda.current_stream(cuda_dev).wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        V, I = topk_sae_cuda_exact(X, W, b, k)
+    for i in range(4):
+        Xn, _, _ = make_inputs(B, d, F, torch.bfloat16, seed=400 + i, device=cuda_dev)
+        if i == 2:
+            Xn = Xn * 1e-3   # thresholds far below the previous replay's
+        X.copy_(Xn)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        Vg, Ig = V.clone(), I.clone()
+        S = oracle.scores_f64(_np(X), _np(W), _np(b))
+        check_against_scores(Vg.cpu().numpy(), Ig.cpu().numpy(), S, k, tol_of("bf16"), f"replay {i}")
+        Ve, Ie = topk_sae_cuda_exact(X, W, b, k)
+        torch.cuda.synchronize()
+        assert torch.equal(Ve, Vg) and torch.equal(Ie, Ig), f"replay {i} differs from the eager call"
