@@ -78,3 +78,36 @@ def test_noalloc_rejects_oversized_problem(cuda_dev):
                                        _lib.STK_DTYPE_BF16, _stream())
     assert rc == 3
     assert "static scratch" in lib.stk_last_error().decode()
+
+
+def test_noalloc_graph_replays(cuda_dev):
+    """The entry point's intended caller: code under graph capture.  Captured
+    once on a side stream, replayed with new inputs, with eager calls of the
+    same entry point on the same static scratch between the replays; every
+    replay must equal stk_exact_forward on its inputs, bit for bit."""
+    B, d, F, k = 128, 256, 65536, 32
+    print(f"case noalloc graph B={B} d={d} F={F} k={k}", flush=True)
+    X, W, b = make_inputs(B, d, F, torch.bfloat16, seed=23, device=cuda_dev)
+    s = torch.cuda.Stream(cuda_dev)
+    s.wait_stream(torch.cuda.current_stream(cuda_dev))
+    with torch.cuda.stream(s):
+        _no_alloc(X, W, b, k)                 # resolves the scratch address outside the capture
+    torch.cuda.current_stream(cuda_dev).wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        V, I = _no_alloc(X, W, b, k)
+    for i in range(3):
+        Xn, _, _ = make_inputs(B, d, F, torch.bfloat16, seed=500 + i, device=cuda_dev)
+        if i == 1:
+            Xn = Xn * 1e-3   # thresholds far below the previous replay's
+        X.copy_(Xn)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        Vg, Ig = V.clone(), I.clone()
+        Vw, Iw = _with_workspace(X, W, b, k)
+        Ve, Ie = _no_alloc(X, W, b, k)
+        torch.cuda.synchronize()
+        assert torch.equal(Vg, Vw) and torch.equal(Ig, Iw), f"replay {i} differs from stk_exact_forward"
+        assert torch.equal(Ve, Vw) and torch.equal(Ie, Iw), f"eager call after replay {i} differs"
