@@ -186,6 +186,7 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
         int64_t nr = ncu / p.nbc;
         if (nr < 1) nr = 1;
         if (nr >= 8) nr &= ~(int64_t)7;
+        if (nr > kMergeMaxSeg) nr = kMergeMaxSeg;   // the merge's segments per row
         p.tpw = cdiv(p.num_tiles, nr);
         p.nwg = (int)nr;
     } else {
@@ -481,7 +482,7 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         if (e != hipSuccess) return hip_fail(e, "mainl_kernel launch");
         mg.list_keys = list_keys; mg.list_cnt = list_cnt; mg.list_cap = p.list_cap;
         mg.head_span = p.head_span; mg.nseg = p.nwg; mg.seg_cap = p.cap; mg.seg_cnt = ml.seg_cnt;
-        mg.spec = 0;
+        mg.spec = p.nwg <= kMergeSegSmall ? 0 : 7;
     } else {
         MainArgs ma;
         std::memset(&ma, 0, sizeof ma);

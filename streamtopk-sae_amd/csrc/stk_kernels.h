@@ -206,6 +206,7 @@ struct MainLArgs {
 // seg_cnt[row * nseg + s] keys at its front.  With nseg == 0 the row is the
 // dense list [0, list_cnt[row * kCntStride]).
 constexpr int kMergeMaxSeg = 1024;
+constexpr int kMergeSegSmall = 256;   // the most segments of merge spec 0 (four workgroups per CU)
 
 struct MergeArgs {
     const uint64_t* list_keys;   // [B][list_cap]
@@ -214,7 +215,8 @@ struct MergeArgs {
     int nseg, seg_cap;
     const int32_t* seg_cnt;      // [B][nseg]
     int k;
-    int spec;                    // 0: chunks of 16 candidates per thread; a list
+    int spec;                    // 0: chunks of 16 candidates per thread, at most
+                                 //   kMergeSegSmall segments (7: up to kMergeMaxSeg); a list
                                  //   expected to hold more than 4096 candidates
                                  //   (32 per thread and chunk): 1 dense, 2 segmented;
                                  //   6, 3, 4, 5: merge_seg_kernel (head <= 256 keys, two

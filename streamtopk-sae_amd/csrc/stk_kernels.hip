@@ -714,12 +714,18 @@ __device__ __forceinline__ bool merge_marked(const MergeArgs& a, int64_t row, in
     return true;
 }
 
-template <int kPer, int kSpec, int NT>
-__global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a)
+// kMaxSeg: the most segments a row may have (the host picks the instance).
+// kWaves: the waves per SIMD the registers must allow (1: no bound); with
+// kMaxSeg = 256 the LDS and registers of the 16-slot instance leave room for
+// four workgroups per CU, so a large batch's rows run in one round.
+template <int kPer, int kSpec, int NT, int kMaxSeg, int kWaves>
+__global__ __launch_bounds__(NT, kWaves) void merge_kernel(MergeArgs a)
 {
+    constexpr int NW = NT / 64;
+    constexpr int kSegPer = (kMaxSeg + NT - 1) / NT;   // segment counts per thread
     __shared__ SelSharedT<NT> S;
-    __shared__ int scnt[kMergeMaxSeg];
-    __shared__ int spre[kMergeMaxSeg];   // inclusive prefix sums of scnt
+    __shared__ int spre[kMaxSeg];   // inclusive prefix sums of the segment counts
+    __shared__ int wsum[NW];
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
     if (merge_marked<NT>(a, row, tid)) return;
@@ -733,61 +739,82 @@ __global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a)
         const int64_t i = tid + (int64_t)u * NT;
         v[u] = keys[i < a.list_cap ? i : a.list_cap - 1];
     }
-    for (int sg = tid; sg < nseg; sg += NT) scnt[sg] = a.seg_cnt[row * nseg + sg];
+    // thread t holds the counts of segments t * kSegPer ..; their inclusive
+    // prefix sums go to spre (a scan over the lanes, then over the waves)
+    int cs[kSegPer];
+    int tsum = 0;
+#pragma unroll
+    for (int e = 0; e < kSegPer; ++e) {
+        const int sg = tid * kSegPer + e;
+        cs[e] = sg < nseg ? a.seg_cnt[row * nseg + sg] : 0;
+        tsum += cs[e];
+    }
     if (tid == 0) S.cnt = 0;
-    __syncthreads();
     // Candidate i (0 <= i < n) is head key i for i < hc, else key i - hc of
     // the segments' valid keys taken in order: the chunks run over valid keys
     // only, however full the segments are.
     int64_t n = hc;
     int top = 0;   // largest power of two <= nseg
     if (nseg > 0) {
-        if (tid < 64) {
-            int carry = 0;
-            for (int s0 = 0; s0 < nseg; s0 += 64) {
-                int c = s0 + tid < nseg ? scnt[s0 + tid] : 0;
+        const int lane = tid & 63, wave = tid >> 6;
+        int x = tsum;
 #pragma unroll
-                for (int o = 1; o < 64; o <<= 1) {
-                    const int t = __shfl_up(c, o);
-                    if (tid >= o) c += t;
-                }
-                if (s0 + tid < nseg) spre[s0 + tid] = carry + c;
-                carry += __shfl(c, 63);
-            }
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(x, o, 64);
+            if (lane >= o) x += t;
+        }
+        if (lane == 63) wsum[wave] = x;
+        __syncthreads();
+        int c = x - tsum;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) c += w < wave ? wsum[w] : 0;
+#pragma unroll
+        for (int e = 0; e < kSegPer; ++e) {
+            const int sg = tid * kSegPer + e;
+            c += cs[e];
+            if (sg < nseg) spre[sg] = c;
         }
         __syncthreads();
         n = hc + spre[nseg - 1];
         top = 1 << (31 - __builtin_clz(nseg));
+    } else {
+        __syncthreads();
     }
     uint64_t run = 0;
     for (int64_t c0 = 0; c0 < n; c0 += (int64_t)kPer * NT) {
         if (nseg > 0) {
             // segment of each segment candidate: the number of segments whose
-            // inclusive prefix is <= its index (all items searched in step)
-            int j[kPer], pos[kPer];
+            // inclusive prefix is <= its index (kGrp items searched in step;
+            // a group's loads are in flight while the next group searches)
+            constexpr int kGrp = kPer < 8 ? kPer : 8;
+            static_assert(kPer % kGrp == 0, "whole groups");
 #pragma unroll
-            for (int u = 0; u < kPer; ++u) {
-                j[u] = (int)(c0 + tid + (int64_t)u * NT - hc);
-                pos[u] = 0;
-            }
-            for (int st = top; st > 0; st >>= 1) {
+            for (int g0 = 0; g0 < kPer; g0 += kGrp) {
+                int j[kGrp], pos[kGrp];
 #pragma unroll
-                for (int u = 0; u < kPer; ++u) {
-                    const int q = pos[u] + st - 1;
-                    if (q < nseg && spre[q] <= j[u]) pos[u] += st;
+                for (int u = 0; u < kGrp; ++u) {
+                    j[u] = (int)(c0 + tid + (int64_t)(g0 + u) * NT - hc);
+                    pos[u] = 0;
                 }
-            }
+                for (int st = top; st > 0; st >>= 1) {
 #pragma unroll
-            for (int u = 0; u < kPer; ++u) {
-                const int64_t i = c0 + tid + (int64_t)u * NT;
-                if (i >= n) {
-                    v[u] = 0ull;
-                } else if (i < hc) {
-                    v[u] = keys[i];
-                } else {
-                    const int sg = pos[u];
-                    const int off = j[u] - (spre[sg] - scnt[sg]);
-                    v[u] = keys[a.head_span + (int64_t)sg * a.seg_cap + off];
+                    for (int u = 0; u < kGrp; ++u) {
+                        const int q = pos[u] + st - 1;
+                        if (q < nseg && spre[q] <= j[u]) pos[u] += st;
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < kGrp; ++u) {
+                    const int64_t i = c0 + tid + (int64_t)(g0 + u) * NT;
+                    if (i >= n) {
+                        v[g0 + u] = 0ull;
+                    } else if (i < hc) {
+                        v[g0 + u] = keys[i];
+                    } else {
+                        const int sg = pos[u];
+                        const int off = j[u] - (sg > 0 ? spre[sg - 1] : 0);
+                        v[g0 + u] = keys[a.head_span + (int64_t)sg * a.seg_cap + off];
+                    }
                 }
             }
         } else {
@@ -1068,9 +1095,11 @@ hipError_t launch_merge(const MergeArgs& a, int64_t rows, hipStream_t st)
     // otherwise 16 slots per thread, which also keeps the registers low enough
     // for four workgroups per CU when the rows are many (large batches)
     if (a.spec == 1)
-        launch(merge_kernel<32, 16, kThreads>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+        launch(merge_kernel<32, 16, kThreads, kMergeMaxSeg, 1>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     else if (a.spec == 2)
-        launch(merge_kernel<32, 0, kThreads>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+        launch(merge_kernel<32, 0, kThreads, kMergeMaxSeg, 1>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+    else if (a.spec == 7)   // more segments than the 16-slot instance below takes
+        launch(merge_kernel<16, 0, kThreads, kMergeMaxSeg, 1>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     else if (a.spec == 6)   // segments expected to hold up to ~3 keys: 8 per pass
         launch(merge_seg_kernel<4, 4, 2 * kThreads>, dim3((unsigned)rows), dim3(2 * kThreads), 0, st, a);
     else if (a.spec == 3)   // segments expected to hold up to ~12 keys: 32 per pass
@@ -1080,7 +1109,7 @@ hipError_t launch_merge(const MergeArgs& a, int64_t rows, hipStream_t st)
     else if (a.spec == 5)   // fuller segments: 64 per pass
         launch(merge_seg_kernel<32, 8, 2 * kThreads>, dim3((unsigned)rows), dim3(2 * kThreads), 0, st, a);
     else
-        launch(merge_kernel<16, 0, kThreads>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+        launch(merge_kernel<16, 0, kThreads, kMergeSegSmall, 4>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     return hipGetLastError();
 }
 

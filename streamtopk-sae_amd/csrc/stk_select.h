@@ -16,8 +16,10 @@ struct SelSharedT {
     static constexpr int NW = NT / 64;
     uint64_t buf[kSelCap];
     uint32_t hist[NW][256];
-    uint64_t sel[kMaxK];
-    uint64_t tmax[NT];
+    union {                  // never live together: each use ends at a barrier
+        uint64_t sel[kMaxK];   // select_compact's kept keys
+        uint64_t tmax[NT];     // kth_of_maxima's per-thread maxima
+    };
     uint64_t wthr[NW];
     uint64_t prefix, mask, thr;
     uint32_t remaining;
@@ -79,12 +81,12 @@ __device__ inline uint64_t kth_of_maxima(SelSharedT<NT>& S, uint64_t m, int k, i
         int r = 0;
         const uint64_t* wm = S.tmax + wave * 64;
 #pragma unroll
-        for (int i = 0; i < 64; i += 16) {
-            u64x2 v[8];
+        for (int i = 0; i < 64; i += 8) {
+            u64x2 v[4];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = *(const u64x2*)(wm + i + 2 * u);
+            for (int u = 0; u < 4; ++u) v[u] = *(const u64x2*)(wm + i + 2 * u);
 #pragma unroll
-            for (int u = 0; u < 8; ++u) r += (int)(v[u][0] > m) + (int)(v[u][1] > m);
+            for (int u = 0; u < 4; ++u) r += (int)(v[u][0] > m) + (int)(v[u][1] > m);
         }
         // keys are distinct, so exactly one non-zero maximum has rank kw - 1
         const uint64_t hit = __ballot(m != 0 && r == kw - 1);
