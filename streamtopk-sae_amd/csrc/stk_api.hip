@@ -482,7 +482,10 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         if (e != hipSuccess) return hip_fail(e, "mainl_kernel launch");
         mg.list_keys = list_keys; mg.list_cnt = list_cnt; mg.list_cap = p.list_cap;
         mg.head_span = p.head_span; mg.nseg = p.nwg; mg.seg_cap = p.cap; mg.seg_cnt = ml.seg_cnt;
-        mg.spec = p.nwg <= kMergeSegSmall ? 0 : 7;
+        // without a head (the exchange) the segments are read in place, four
+        // threads each; else each key's segment is searched for over the
+        // counts' prefix sums
+        mg.spec = p.head_span == 0 ? 8 : p.nwg <= kMergeSegSmall ? 0 : 7;
     } else {
         MainArgs ma;
         std::memset(&ma, 0, sizeof ma);

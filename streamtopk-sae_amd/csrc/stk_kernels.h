@@ -220,7 +220,9 @@ struct MergeArgs {
                                  //   expected to hold more than 4096 candidates
                                  //   (32 per thread and chunk): 1 dense, 2 segmented;
                                  //   6, 3, 4, 5: merge_seg_kernel (head <= 256 keys, two
-                                 //   threads per segment; 8, 32, 48 or 64 keys per pass)
+                                 //   threads per segment; 8, 32, 48 or 64 keys per pass);
+                                 //   8: merge_seg_kernel for a list without a head, four
+                                 //   threads per segment, 64 keys per pass, 256 threads
     int32_t f_offset;            // added to every emitted index (a shard's first latent)
     int ties;                    // non-zero: keys may repeat (stk_topk_merge's parts); equal keys
                                  //   take consecutive ranks

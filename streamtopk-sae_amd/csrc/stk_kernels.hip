@@ -840,10 +840,11 @@ __global__ __launch_bounds__(NT, kWaves) void merge_kernel(MergeArgs a)
         emit_topk<false>(S, k, tid, out);
 }
 
-// Per row: top-k of main_kernel's list -- a head of at most kThreads keys,
-// then nseg segments of seg_cap slots, segment s holding seg_cnt[row * nseg +
-// s] keys.  NT = SPLIT * kThreads threads; the SPLIT threads of slot t
-// (threads SPLIT * t ..) read segments t, t + kThreads, ..., the keys in
+// Per row: top-k of a segmented list (main_kernel's, or mainl_kernel's
+// without a head) -- a head of at most NT keys, then nseg segments of seg_cap
+// slots, segment s holding seg_cnt[row * nseg + s] keys.  NT = SPLIT * kSlots
+// threads; the SPLIT threads of slot t (threads SPLIT * t ..) read segments
+// t, t + kSlots, ..., the keys in
 // pairs dealt round-robin (pair j of a segment to thread j % SPLIT), kPer keys
 // per thread and pass (16-byte loads, adjacent threads on adjacent pairs):
 // no search for a key's segment, and every thread has its loads in flight at
@@ -851,12 +852,14 @@ __global__ __launch_bounds__(NT, kWaves) void merge_kernel(MergeArgs a)
 // keys per thread of a segment (SPLIT * kEager keys) are loaded without
 // waiting for the counts and masked afterwards.  A pass filters as
 // merge_kernel's chunks.
-template <int kPer, int kEager, int NT>
-__global__ __launch_bounds__(NT) void merge_seg_kernel(MergeArgs a)
+// kWaves: the waves per SIMD the registers must allow (1: no bound).
+// kHead false: the list has no head (head_span == 0, host).
+template <int kPer, int kEager, int NT, int SPLIT, int kWaves, bool kHead>
+__global__ __launch_bounds__(NT, kWaves) void merge_seg_kernel(MergeArgs a)
 {
     static_assert(kPer % 2 == 0 && kEager % 2 == 0 && kEager <= kPer, "pairs of keys");
-    static_assert(NT % kThreads == 0, "whole slots");
-    constexpr int SPLIT = NT / kThreads;
+    static_assert(NT % SPLIT == 0, "whole slots");
+    constexpr int kSlots = NT / SPLIT;
     constexpr int kStep = SPLIT * kPer;   // keys of a segment per pass
     __shared__ SelSharedT<NT> S;
     const int tid = threadIdx.x;
@@ -865,14 +868,17 @@ __global__ __launch_bounds__(NT) void merge_seg_kernel(MergeArgs a)
     if (merge_marked<NT>(a, row, tid)) return;
     const int k = a.k;
     const int nseg = a.nseg;
-    const int64_t hs = a.head_span;   // <= kThreads (host)
+    const int64_t hs = kHead ? a.head_span : 0;   // <= NT (host)
     const uint64_t* keys = a.list_keys + row * a.list_cap;
-    uint64_t v[kPer + 1];
-    v[kPer] = tid < hs ? keys[tid] : 0ull;   // the head key rides in the first pass
-    const int hc = hs > 0 ? a.list_cnt[row * kCntStride] : 0;
+    uint64_t v[kHead ? kPer + 1 : kPer];
+    int hc = 0;
+    if constexpr (kHead) {
+        v[kPer] = tid < hs ? keys[tid] : 0ull;   // the head key rides in the first pass
+        hc = hs > 0 ? a.list_cnt[row * kCntStride] : 0;
+    }
     if (tid == 0) S.cnt = 0;
     uint64_t run = 0;
-    for (int s0 = 0; s0 < nseg || s0 == 0; s0 += kThreads) {
+    for (int s0 = 0; s0 < nseg || s0 == 0; s0 += kSlots) {
         const int sg = s0 + slot;
         const bool own = sg < nseg;
         // segment starts are 16-byte aligned (head_span and seg_cap even);
@@ -886,7 +892,8 @@ __global__ __launch_bounds__(NT) void merge_seg_kernel(MergeArgs a)
             if (own && SPLIT * u + 2 * part < a.seg_cap) e[u / 2] = *(const u64x2*)(q + SPLIT * u);
         }
         const int cnt = (own ? a.seg_cnt[row * nseg + sg] : 0) - 2 * part;
-        if (s0 == 0 && tid >= hc) v[kPer] = 0ull;
+        if constexpr (kHead)
+            if (s0 == 0 && tid >= hc) v[kPer] = 0ull;
         for (int base = 0;; base += kStep) {
 #pragma unroll
             for (int u = 0; u < kPer; u += 2) {
@@ -902,7 +909,7 @@ __global__ __launch_bounds__(NT) void merge_seg_kernel(MergeArgs a)
                 v[u + 1] = o + 1 < cnt ? p[1] : 0ull;
             }
             merge_pass(S, v, k, tid, run);
-            v[kPer] = 0ull;
+            if constexpr (kHead) v[kPer] = 0ull;
             if (!__syncthreads_or(cnt > base + kStep - 2 * part)) break;
         }
     }
@@ -1101,13 +1108,16 @@ hipError_t launch_merge(const MergeArgs& a, int64_t rows, hipStream_t st)
     else if (a.spec == 7)   // more segments than the 16-slot instance below takes
         launch(merge_kernel<16, 0, kThreads, kMergeMaxSeg, 1>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     else if (a.spec == 6)   // segments expected to hold up to ~3 keys: 8 per pass
-        launch(merge_seg_kernel<4, 4, 2 * kThreads>, dim3((unsigned)rows), dim3(2 * kThreads), 0, st, a);
+        launch(merge_seg_kernel<4, 4, 2 * kThreads, 2, 1, true>, dim3((unsigned)rows), dim3(2 * kThreads), 0, st, a);
     else if (a.spec == 3)   // segments expected to hold up to ~12 keys: 32 per pass
-        launch(merge_seg_kernel<16, 8, 2 * kThreads>, dim3((unsigned)rows), dim3(2 * kThreads), 0, st, a);
+        launch(merge_seg_kernel<16, 8, 2 * kThreads, 2, 1, true>, dim3((unsigned)rows), dim3(2 * kThreads), 0, st, a);
     else if (a.spec == 4)   // segments expected to hold up to ~24 keys: 48 per pass
-        launch(merge_seg_kernel<24, 8, 2 * kThreads>, dim3((unsigned)rows), dim3(2 * kThreads), 0, st, a);
+        launch(merge_seg_kernel<24, 8, 2 * kThreads, 2, 1, true>, dim3((unsigned)rows), dim3(2 * kThreads), 0, st, a);
     else if (a.spec == 5)   // fuller segments: 64 per pass
-        launch(merge_seg_kernel<32, 8, 2 * kThreads>, dim3((unsigned)rows), dim3(2 * kThreads), 0, st, a);
+        launch(merge_seg_kernel<32, 8, 2 * kThreads, 2, 1, true>, dim3((unsigned)rows), dim3(2 * kThreads), 0, st, a);
+    else if (a.spec == 8)   // no head, few segments (a large batch's): 4 threads per segment, 64 keys
+                            // per pass, four row workgroups per CU
+        launch(merge_seg_kernel<16, 4, kThreads, 4, 4, false>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     else
         launch(merge_kernel<16, 0, kThreads, kMergeSegSmall, 4>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     return hipGetLastError();
