@@ -186,7 +186,7 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
         int64_t nr = ncu / p.nbc;
         if (nr < 1) nr = 1;
         if (nr >= 8) nr &= ~(int64_t)7;
-        if (nr > kMergeMaxSeg) nr = kMergeMaxSeg;   // the merge's segments per row
+        if (nr > kMergeMaxSeg) nr = kMergeMaxSeg;   // merge_kernel's segments per row
         p.tpw = cdiv(p.num_tiles, nr);
         p.nwg = (int)nr;
     } else {
@@ -485,7 +485,7 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
         // without a head (the exchange) the segments are read in place, four
         // threads each; else each key's segment is searched for over the
         // counts' prefix sums
-        mg.spec = p.head_span == 0 ? 8 : p.nwg <= kMergeSegSmall ? 0 : 7;
+        mg.spec = p.head_span == 0 ? 8 : 0;
     } else {
         MainArgs ma;
         std::memset(&ma, 0, sizeof ma);

@@ -205,8 +205,7 @@ struct MainLArgs {
 // front; then nseg segments of seg_cap slots, segment s holding
 // seg_cnt[row * nseg + s] keys at its front.  With nseg == 0 the row is the
 // dense list [0, list_cnt[row * kCntStride]).
-constexpr int kMergeMaxSeg = 1024;
-constexpr int kMergeSegSmall = 256;   // the most segments of merge spec 0 (four workgroups per CU)
+constexpr int kMergeMaxSeg = 256;   // merge_kernel's segments per row (mainl_kernel's W ranges)
 
 struct MergeArgs {
     const uint64_t* list_keys;   // [B][list_cap]
@@ -215,10 +214,9 @@ struct MergeArgs {
     int nseg, seg_cap;
     const int32_t* seg_cnt;      // [B][nseg]
     int k;
-    int spec;                    // 0: chunks of 16 candidates per thread, at most
-                                 //   kMergeSegSmall segments (7: up to kMergeMaxSeg); a list
-                                 //   expected to hold more than 4096 candidates
-                                 //   (32 per thread and chunk): 1 dense, 2 segmented;
+    int spec;                    // 0: merge_kernel, chunks of 16 candidates per thread;
+                                 //   1: merge_kernel for a dense list expected to hold more
+                                 //   than 4096 candidates (32 per thread and chunk);
                                  //   6, 3, 4, 5: merge_seg_kernel (head <= 256 keys, two
                                  //   threads per segment; 8, 32, 48 or 64 keys per pass);
                                  //   8: merge_seg_kernel for a list without a head, four

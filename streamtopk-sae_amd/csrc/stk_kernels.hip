@@ -714,17 +714,17 @@ __device__ __forceinline__ bool merge_marked(const MergeArgs& a, int64_t row, in
     return true;
 }
 
-// kMaxSeg: the most segments a row may have (the host picks the instance).
-// kWaves: the waves per SIMD the registers must allow (1: no bound); with
-// kMaxSeg = 256 the LDS and registers of the 16-slot instance leave room for
-// four workgroups per CU, so a large batch's rows run in one round.
-template <int kPer, int kSpec, int NT, int kMaxSeg, int kWaves>
+// At most kMergeMaxSeg segments per row (host), one count per thread.
+// kWaves: the waves per SIMD the registers must allow (1: no bound); the LDS
+// and registers of the 16-slot instance leave room for four workgroups per
+// CU, so a large batch's rows run in one round.
+template <int kPer, int kSpec, int NT, int kWaves>
 __global__ __launch_bounds__(NT, kWaves) void merge_kernel(MergeArgs a)
 {
     constexpr int NW = NT / 64;
-    constexpr int kSegPer = (kMaxSeg + NT - 1) / NT;   // segment counts per thread
+    static_assert(kMergeMaxSeg <= NT, "one segment count per thread");
     __shared__ SelSharedT<NT> S;
-    __shared__ int spre[kMaxSeg];   // inclusive prefix sums of the segment counts
+    __shared__ int spre[kMergeMaxSeg];   // inclusive prefix sums of the segment counts
     __shared__ int wsum[NW];
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
@@ -739,16 +739,9 @@ __global__ __launch_bounds__(NT, kWaves) void merge_kernel(MergeArgs a)
         const int64_t i = tid + (int64_t)u * NT;
         v[u] = keys[i < a.list_cap ? i : a.list_cap - 1];
     }
-    // thread t holds the counts of segments t * kSegPer ..; their inclusive
-    // prefix sums go to spre (a scan over the lanes, then over the waves)
-    int cs[kSegPer];
-    int tsum = 0;
-#pragma unroll
-    for (int e = 0; e < kSegPer; ++e) {
-        const int sg = tid * kSegPer + e;
-        cs[e] = sg < nseg ? a.seg_cnt[row * nseg + sg] : 0;
-        tsum += cs[e];
-    }
+    // thread t holds the count of segment t; the inclusive prefix sums go to
+    // spre (a scan over the lanes, then over the waves)
+    const int cs = tid < nseg ? a.seg_cnt[row * nseg + tid] : 0;
     if (tid == 0) S.cnt = 0;
     // Candidate i (0 <= i < n) is head key i for i < hc, else key i - hc of
     // the segments' valid keys taken in order: the chunks run over valid keys
@@ -757,7 +750,7 @@ __global__ __launch_bounds__(NT, kWaves) void merge_kernel(MergeArgs a)
     int top = 0;   // largest power of two <= nseg
     if (nseg > 0) {
         const int lane = tid & 63, wave = tid >> 6;
-        int x = tsum;
+        int x = cs;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const int t = __shfl_up(x, o, 64);
@@ -765,15 +758,9 @@ __global__ __launch_bounds__(NT, kWaves) void merge_kernel(MergeArgs a)
         }
         if (lane == 63) wsum[wave] = x;
         __syncthreads();
-        int c = x - tsum;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) c += w < wave ? wsum[w] : 0;
-#pragma unroll
-        for (int e = 0; e < kSegPer; ++e) {
-            const int sg = tid * kSegPer + e;
-            c += cs[e];
-            if (sg < nseg) spre[sg] = c;
-        }
+        for (int w = 0; w < NW; ++w) x += w < wave ? wsum[w] : 0;
+        if (tid < nseg) spre[tid] = x;
         __syncthreads();
         n = hc + spre[nseg - 1];
         top = 1 << (31 - __builtin_clz(nseg));
@@ -1097,16 +1084,12 @@ hipError_t launch_pack(const PackArgs& a, int64_t rows, hipStream_t st)
 
 hipError_t launch_merge(const MergeArgs& a, int64_t rows, hipStream_t st)
 {
-    // lists expected to exceed one 4096-slot chunk: 32 slots per thread (one
-    // chunk); a dense one (spec 1) has its first 16 loaded ahead of the count;
-    // otherwise 16 slots per thread, which also keeps the registers low enough
-    // for four workgroups per CU when the rows are many (large batches)
+    // dense lists expected to exceed one 4096-slot chunk (spec 1): 32 slots
+    // per thread (one chunk), the first 16 loaded ahead of the count; spec 0:
+    // 16 slots per thread, which also keeps the registers low enough for four
+    // workgroups per CU when the rows are many (large batches)
     if (a.spec == 1)
-        launch(merge_kernel<32, 16, kThreads, kMergeMaxSeg, 1>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
-    else if (a.spec == 2)
-        launch(merge_kernel<32, 0, kThreads, kMergeMaxSeg, 1>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
-    else if (a.spec == 7)   // more segments than the 16-slot instance below takes
-        launch(merge_kernel<16, 0, kThreads, kMergeMaxSeg, 1>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+        launch(merge_kernel<32, 16, kThreads, 1>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     else if (a.spec == 6)   // segments expected to hold up to ~3 keys: 8 per pass
         launch(merge_seg_kernel<4, 4, 2 * kThreads, 2, 1, true>, dim3((unsigned)rows), dim3(2 * kThreads), 0, st, a);
     else if (a.spec == 3)   // segments expected to hold up to ~12 keys: 32 per pass
@@ -1119,7 +1102,7 @@ hipError_t launch_merge(const MergeArgs& a, int64_t rows, hipStream_t st)
                             // per pass, four row workgroups per CU
         launch(merge_seg_kernel<16, 4, kThreads, 4, 4, false>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     else
-        launch(merge_kernel<16, 0, kThreads, kMergeSegSmall, 4>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
+        launch(merge_kernel<16, 0, kThreads, 4>, dim3((unsigned)rows), dim3(kThreads), 0, st, a);
     return hipGetLastError();
 }
 
