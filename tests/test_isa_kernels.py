@@ -5,7 +5,10 @@ No kernel may use scratch memory (a register spill or an indexed register
 array), including the 512-thread selection kernels (the merge's two threads
 per segment, the large sample's threshold), whose thread count halves the
 registers a lane may hold.  main_kernel (8 waves, two per SIMD) must stay
-within 256 VGPRs per lane.
+within 256 VGPRs per lane.  The merges after mainl_kernel (256 threads) must
+leave room for four workgroups per CU -- at most 128 registers per lane and
+40 KiB of LDS each -- so that a large batch's rows (1024 at config 4, four per
+CU) are merged in one round.
 """
 import os
 import re
@@ -68,3 +71,19 @@ def test_main_kernel_registers(asm):
         if "main_kernel" in n:
             vgpr = int(re.search(r"\.vgpr_count:\s+(\d+)", _meta(asm, n)).group(1))
             assert vgpr <= 256, (n, vgpr)
+
+
+def test_large_batch_merges_four_per_cu(asm):
+    names = _kernels(asm)
+    # merge_kernel<16, 0, 256, 4> (after the sample pass) and
+    # merge_seg_kernel<16, 4, 256, 4, 4, false> (after the exchange)
+    want = ("merge_kernelILi16ELi0ELi256ELi4E", "merge_seg_kernelILi16ELi4ELi256ELi4ELi4ELb0E")
+    for w in want:
+        hits = [n for n in names if w in n]
+        assert len(hits) == 1, (w, hits)
+        meta = _meta(asm, hits[0])
+        vgpr = int(re.search(r"\.vgpr_count:\s+(\d+)", meta).group(1))
+        agpr = int(re.search(r"\.agpr_count:\s+(\d+)", meta).group(1))
+        lds = int(re.search(r"\.group_segment_fixed_size:\s+(\d+)", meta).group(1))
+        assert vgpr + agpr <= 128, (w, vgpr, agpr)
+        assert lds <= 40 * 1024, (w, lds)
