@@ -70,6 +70,7 @@ def _launches(fn):
     (600, 65536, 64, True),      # large batch: mainl_kernel, 80 W ranges x 4 maxima per row
     (4096, 65536, 128, False),   # 16 W ranges x 4 maxima < k: mainl_kernel with a sample pass
     (512, 20000, 64, True),      # 79 tiles over 128 W ranges: the 79 that hold tiles exchange
+    (2048, 65536, 32, True),     # eight row blocks of 32 W ranges; rows merged in two rounds
 ])
 def test_exchange_replaces_threshold_passes(cuda_dev, B, F, k, xch):
     print(f"case launches B={B} F={F} k={k}", flush=True)
@@ -90,6 +91,7 @@ def test_exchange_replaces_threshold_passes(cuda_dev, B, F, k, xch):
     (600, 128, 30000, 64, "bf16"),  # mainl_kernel, three row blocks
     (1024, 256, 65536, 128, "fp16"),
     (512, 64, 20000, 32, "bf16"),   # mainl_kernel with empty W ranges
+    (2048, 64, 65536, 32, "bf16"),  # more rows than one round of the merge's workgroups
 ])
 def test_exchange_waits_run_out(cuda_dev, monkeypatch, B, d, F, k, dtype_name):
     """Every exchange wait runs out at once: thresholds stay 0 and the result is still exact."""
@@ -212,6 +214,7 @@ def _timeouts(X):
     (600, 128, 65536, 64, True),      # mainl_kernel
     (1024, 256, 262144, 128, False),  # mainl_kernel, config 4's grid
     (512, 64, 20000, 64, True),       # mainl_kernel, 79 of 128 W ranges hold tiles
+    (2048, 768, 65536, 32, False),    # mainl_kernel, eight row blocks of 32 W ranges
 ])
 def test_exchange_never_runs_out(cuda_dev, monkeypatch, B, d, F, k, short_waits):
     """On an idle device every workgroup of the grid is resident, so no poll of
