@@ -22,10 +22,13 @@
  *     when it is allocated), and again after a call on it returned an error;
  *     every successful call leaves it valid for the next call of any shape,
  *     also when the calls are replays of a captured HIP graph.  Calls that
- *     overlap in time must not share a workspace.  (The exact path's
+ *     overlap in time must not share a workspace.  One workspace may serve
+ *     exact, approximate and shard-merge calls in turn.  (The exact path's
  *     workgroups exchange per-row thresholds through words tagged with the
- *     call's number, kept in the workspace's first 256 bytes and advanced by
- *     each call on the device; zero is never a call's tag.)
+ *     call's number, kept in the workspace's first 256 bytes -- which only
+ *     exact calls write -- and advanced by each exact call on the device,
+ *     modulo 2^22 - 1; zero is never a call's tag, and each call's merge
+ *     zeroes the words it tagged.)
  */
 #ifndef STREAMTOPK_H
 #define STREAMTOPK_H
@@ -121,7 +124,8 @@ int stk_topk_merge(const float* Vp, const int32_t* Ip, int64_t nparts, int64_t B
 
 /* Device workspace (bytes) for stk_approx_forward.  `with_candidates` is
  * non-zero when the caller passes a candidate buffer (then the workspace holds
- * each group's first candidate as an 8-byte key: B * ceil(F/128) * 8 bytes). */
+ * 256 bytes, then each group's first candidate as an 8-byte key:
+ * 256 + B * ceil(F/128) * 8 bytes). */
 int stk_approx_workspace_bytes(int64_t B, int64_t d, int64_t F, int64_t k, int64_t c, int dtype,
                                int with_candidates, size_t* out_bytes);
 

@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -149,6 +150,28 @@ static int cu_count(int* out)
     return 0;
 }
 
+// ---------------------------------------------------------------------------
+// Test hooks (stk_test_set_hooks, exported for the test suite and not
+// declared in include/streamtopk.h): they force paths that real inputs never
+// take -- the sample pass at shapes that would exchange thresholds, a retry
+// bound low enough to be reached, exchange waits that run out.  Set from the
+// host, read once per call; the defaults are the product's behaviour.
+// ---------------------------------------------------------------------------
+struct TestHooks {
+    int no_xch = 0;              // non-zero: never take the threshold exchange
+    int max_rounds = -1;         // >= 0: the streaming kernels' retry bound
+    int64_t xch_wait = kXchWaitTicks;   // the exchange's poll bound in ticks (0: one
+                                        // poll; < 0: none, every threshold 0)
+};
+static std::mutex g_hooks_mu;
+static TestHooks g_hooks;
+
+static TestHooks test_hooks()
+{
+    std::lock_guard<std::mutex> lock(g_hooks_mu);
+    return g_hooks;
+}
+
 static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 static int ilog2_floor(int64_t x) { int l = 0; while ((x >> (l + 1)) > 0) ++l; return l; }
@@ -171,7 +194,8 @@ struct ExactPlan {
     size_t off_thr, off_list, off_lcnt, off_seg, off_xmax, off_xthr, total;
 };
 
-static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int dtype, int ncu)
+static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int dtype, int ncu,
+                                 const TestHooks& hooks)
 {
     ExactPlan p;
     p.num_tiles = cdiv(F, kTileLatents);
@@ -214,7 +238,7 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
     // workgroups.  Measured (B = 512-2048, d = 2048-4096, k = 64-128): the
     // exchange was 3-8 % faster where it passes fewer latents, 1-4 % slower
     // where it passes ~1.4x as many, and up to 2x slower at n = k.
-    // (STK_TEST_NO_XCH, a test hook read at each call, selects the sample pass.)
+    // (The no_xch test hook selects the sample pass.)
     const int samp_n = (p.large && F >= kSampleLargeMinF) ? kSampleLarge : kSampleTarget;
     {
         // mainl_kernel: the W ranges that hold tiles (main_kernel has no empty workgroup)
@@ -232,7 +256,7 @@ static ExactPlan make_exact_plan(int64_t B, int64_t d, int64_t F, int64_t k, int
             const double ps = (double)k / (double)samp_n;
             ok = px <= (p.large ? 1.0 : 2.0) * ps;
         }
-        p.xch = ok && !std::getenv("STK_TEST_NO_XCH");
+        p.xch = ok && !hooks.no_xch;
     }
     p.sample = F >= kSampleMinF && !p.xch;
     p.samp_log2 = 0;
@@ -381,9 +405,9 @@ static int validate_exact(int64_t B, int64_t d, int64_t F, int64_t k, int dtype)
 }
 
 // Runs sample -> thr -> main -> merge on `st`.
-static int run_exact(const ExactPlan& p, const void* X, const void* W, const float* b, float* V, int32_t* I,
-                     int64_t B, int64_t d, int64_t F, int64_t k, int dtype, unsigned char* ws, hipStream_t st,
-                     int64_t f_offset = 0)
+static int run_exact(const ExactPlan& p, const TestHooks& hooks, const void* X, const void* W, const float* b,
+                     float* V, int32_t* I, int64_t B, int64_t d, int64_t F, int64_t k, int dtype, unsigned char* ws,
+                     hipStream_t st, int64_t f_offset = 0)
 {
     const int dt = dtype;   // STK_DTYPE_* and DT_* share values
     hipError_t e;
@@ -396,13 +420,10 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     uint32_t* xto = epoch + 1;
     uint64_t* err = (uint64_t*)(ws + 8);
     uint64_t* cur = (uint64_t*)(ws + 16);
-    // STK_TEST_MAX_ROUNDS: the test hook that lowers the retry bounds;
-    // STK_TEST_XCH_WAIT: the exchange's wait in ticks (0: every wait runs out
-    // at once, the path of workgroups that were never resident)
-    int max_rounds = -1;
-    if (const char* env = std::getenv("STK_TEST_MAX_ROUNDS")) max_rounds = std::atoi(env);
-    int64_t xwait = kXchWaitTicks;
-    if (const char* env = std::getenv("STK_TEST_XCH_WAIT")) xwait = std::atoll(env);
+    // test hooks: a lower retry bound; the exchange's wait in ticks (0: one
+    // poll, < 0: none -- the paths of workgroups that were never resident)
+    const int max_rounds = hooks.max_rounds;
+    const int64_t xwait = hooks.xch_wait;
     // the sample's partial sums: in each row's segment area, split after split
     float* P = p.sample ? (float*)(list_keys + p.head_span) : nullptr;
     const int64_t p_row = 2 * p.list_cap, p_split = p.nsamp;
@@ -526,6 +547,11 @@ static int run_exact(const ExactPlan& p, const void* X, const void* W, const flo
     mg.err = err;
     mg.cur = cur;
     mg.epoch = epoch;
+    // the exchange's words of this call, zeroed by the merge: row r's maxima
+    // at xmax + r * (words per row), its threshold at xthr + r
+    mg.xmax = p.xch ? (uint64_t*)(ws + p.off_xmax) : nullptr;
+    mg.xthr = p.xch ? (uint64_t*)(ws + p.off_xthr) : nullptr;
+    mg.xmax_row = p.xch ? (p.large ? cdiv(p.num_tiles, p.tpw) * kLXchPerWg : (int64_t)p.nwg) : 0;
     mg.ties = 0;   // one encode's keys are distinct
     mg.V = V; mg.I = I;
     const int pg = prof_begin("merge_kernel", st);
@@ -593,8 +619,9 @@ __attribute__((used)) static __device__ __align__(256) unsigned char scratch[STK
 
 static std::mutex g_scratch_mu;
 static void* g_scratch_ptr[64];   // per device
+static std::atomic<bool> g_scratch_dirty[64];   // per device: zero-fill before the next call
 
-static int scratch_ptr(void** out)
+static int scratch_ptr(void** out, int* out_dev)
 {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -610,6 +637,7 @@ static int scratch_ptr(void** out)
         g_scratch_ptr[dev] = ptr;
     }
     *out = g_scratch_ptr[dev];
+    *out_dev = dev;
     return 0;
 }
 
@@ -631,7 +659,7 @@ int stk_exact_workspace_bytes(int64_t B, int64_t d, int64_t F, int64_t k, int dt
     if (rc) return rc;
     int ncu = 0;
     if ((rc = cu_count(&ncu))) return rc;
-    *out_bytes = (B == 0) ? 0 : make_exact_plan(B, d, F, k, dtype, ncu).total;
+    *out_bytes = (B == 0) ? 0 : make_exact_plan(B, d, F, k, dtype, ncu, test_hooks()).total;
     return 0;
 }
 
@@ -646,12 +674,13 @@ int stk_exact_forward(const void* X, const void* W, const float* b, float* V, in
     if ((rc = check_ptrs(X, W, b, V, I))) return rc;
     int ncu = 0;
     if ((rc = cu_count(&ncu))) return rc;
-    const ExactPlan p = make_exact_plan(B, d, F, k, dtype, ncu);
+    const TestHooks hooks = test_hooks();
+    const ExactPlan p = make_exact_plan(B, d, F, k, dtype, ncu, hooks);
     if (!workspace || workspace_bytes < p.total)
         return set_error(STK_E_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required",
                          workspace ? workspace_bytes : (size_t)0, p.total);
     if ((uintptr_t)workspace & 255) return set_error(STK_E_INVALID, "workspace must be 256-byte aligned");
-    return run_exact(p, X, W, b, V, I, B, d, F, k, dtype, (unsigned char*)workspace, (hipStream_t)stream);
+    return run_exact(p, hooks, X, W, b, V, I, B, d, F, k, dtype, (unsigned char*)workspace, (hipStream_t)stream);
 }
 
 int stk_exact_forward_noalloc(const void* X, const void* W, const float* b, float* V, int32_t* I,
@@ -664,19 +693,32 @@ int stk_exact_forward_noalloc(const void* X, const void* W, const float* b, floa
     if ((rc = check_ptrs(X, W, b, V, I))) return rc;
     int ncu = 0;
     if ((rc = cu_count(&ncu))) return rc;
-    const ExactPlan p = make_exact_plan(B, d, F, k, dtype, ncu);
+    const TestHooks hooks = test_hooks();
+    const ExactPlan p = make_exact_plan(B, d, F, k, dtype, ncu, hooks);
     if (p.total > (size_t)STK_NOALLOC_SCRATCH_BYTES)
         return set_error(STK_E_WORKSPACE,
                          "this problem needs %zu bytes of workspace, more than the %zu-byte static scratch of "
                          "stk_exact_forward_noalloc; call stk_exact_forward with a workspace",
                          p.total, (size_t)STK_NOALLOC_SCRATCH_BYTES);
     void* ws = nullptr;
-    if ((rc = scratch_ptr(&ws))) return rc;
+    int dev = 0;
+    if ((rc = scratch_ptr(&ws, &dev))) return rc;
+    const hipStream_t st = (hipStream_t)stream;
+    // A call that failed after its first launch may have left words tagged
+    // with a tag its merge never retired (the epoch did not advance): the
+    // scratch is zero-filled (a fill kernel, no memset node) before it is
+    // used again.
+    if (g_scratch_dirty[dev].load()) {
+        const hipError_t e = launch_fill_zero(ws, STK_NOALLOC_SCRATCH_BYTES, st);
+        if (e != hipSuccess) return hip_fail(e, "scratch fill launch");
+        g_scratch_dirty[dev].store(false);
+    }
     // no profiling events either (creating one may allocate)
     const int prof = g_prof;
     g_prof = 0;
-    rc = run_exact(p, X, W, b, V, I, B, d, F, k, dtype, (unsigned char*)ws, (hipStream_t)stream);
+    rc = run_exact(p, hooks, X, W, b, V, I, B, d, F, k, dtype, (unsigned char*)ws, st);
     g_prof = prof;
+    if (rc) g_scratch_dirty[dev].store(true);
     return rc;
 }
 
@@ -696,17 +738,16 @@ int stk_exact_forward_shard(const void* X, const void* W, const float* b, float*
     if ((rc = check_ptrs(X, W, b, V, I))) return rc;
     int ncu = 0;
     if ((rc = cu_count(&ncu))) return rc;
-    const ExactPlan p = make_exact_plan(B, d, F, k, dtype, ncu);
+    const TestHooks hooks = test_hooks();
+    const ExactPlan p = make_exact_plan(B, d, F, k, dtype, ncu, hooks);
     if (!workspace || workspace_bytes < p.total)
         return set_error(STK_E_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required",
                          workspace ? workspace_bytes : (size_t)0, p.total);
     if ((uintptr_t)workspace & 255) return set_error(STK_E_INVALID, "workspace must be 256-byte aligned");
-    return run_exact(p, X, W, b, V, I, B, d, F, k, dtype, (unsigned char*)workspace, (hipStream_t)stream,
+    return run_exact(p, hooks, X, W, b, V, I, B, d, F, k, dtype, (unsigned char*)workspace, (hipStream_t)stream,
                      f_offset);
 }
 
-// Merge workspace: the dense candidate lists (nparts*k keys per row) and the
-// per-row counts.
 static int validate_merge(int64_t B, int64_t k, int64_t nparts)
 {
     if (B < 0) return set_error(STK_E_INVALID, "invalid shape: B=%lld", (long long)B);
@@ -718,9 +759,12 @@ static int validate_merge(int64_t B, int64_t k, int64_t nparts)
     return 0;
 }
 
+// Merge workspace: past the control line (which only the exact path
+// writes: a workspace shared with exact calls keeps its epoch), the dense
+// candidate lists (nparts*k keys per row), then the per-row counts.
 static size_t merge_ws_lcnt(int64_t B, int64_t k, int64_t nparts)
 {
-    return ((size_t)B * (size_t)(nparts * k) * 8 + 255) & ~(size_t)255;
+    return kCtlBytes + (((size_t)B * (size_t)(nparts * k) * 8 + 255) & ~(size_t)255);
 }
 
 int stk_topk_merge_workspace_bytes(int64_t B, int64_t k, int64_t nparts, size_t* out_bytes)
@@ -752,7 +796,7 @@ int stk_topk_merge(const float* Vp, const int32_t* Ip, int64_t nparts, int64_t B
     const hipStream_t st = (hipStream_t)stream;
     PackArgs pa;
     pa.V = Vp; pa.I = Ip; pa.B = B; pa.k = (int)k; pa.nparts = (int)nparts;
-    pa.list_keys = (uint64_t*)ws;
+    pa.list_keys = (uint64_t*)(ws + kCtlBytes);
     pa.list_cnt = (int32_t*)(ws + merge_ws_lcnt(B, k, nparts));
     pa.list_cap = nparts * k;
     hipError_t e = launch_pack(pa, B, st);
@@ -782,11 +826,15 @@ int stk_approx_workspace_bytes(int64_t B, int64_t d, int64_t F, int64_t k, int64
     int rc = validate_approx(B, d, F, k, c, dtype);
     if (rc) return rc;
     if (B == 0) { *out_bytes = 0; return 0; }
-    // with a candidate buffer: the groups' head keys, B x ceil(F / 128) words
-    if (with_candidates) { *out_bytes = align256((size_t)B * cdiv(F, kApproxGroup) * 8); return 0; }
+    // with a candidate buffer: past the control line, the groups' head keys,
+    // B x ceil(F / 128) words
+    if (with_candidates) {
+        *out_bytes = kCtlBytes + align256((size_t)B * cdiv(F, kApproxGroup) * 8);
+        return 0;
+    }
     int ncu = 0;
     if ((rc = cu_count(&ncu))) return rc;
-    *out_bytes = make_exact_plan(B, d, F, k, dtype, ncu).total;
+    *out_bytes = make_exact_plan(B, d, F, k, dtype, ncu, test_hooks()).total;
     return 0;
 }
 
@@ -814,15 +862,18 @@ int stk_approx_forward(const void* X, const void* W, const float* b, float* V, i
         // it), so the union of the per-group top-c holds the exact top-k and
         // its top-k is exactly that set: the exact streaming path computes the
         // approximate result without materialising any candidate.
-        const ExactPlan p = make_exact_plan(B, d, F, k, dtype, ncu);
+        const TestHooks hooks = test_hooks();
+        const ExactPlan p = make_exact_plan(B, d, F, k, dtype, ncu, hooks);
         if (!workspace || workspace_bytes < p.total)
             return set_error(STK_E_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required",
                              workspace ? workspace_bytes : (size_t)0, p.total);
         if ((uintptr_t)workspace & 255) return set_error(STK_E_INVALID, "workspace must be 256-byte aligned");
-        return run_exact(p, X, W, b, V, I, B, d, F, k, dtype, (unsigned char*)workspace, st);
+        return run_exact(p, hooks, X, W, b, V, I, B, d, F, k, dtype, (unsigned char*)workspace, st);
     }
     const GroupPlan p = make_group_plan(B, F, ncu);
-    const size_t heads_bytes = (size_t)B * p.num_groups * 8;
+    // the group heads start past the control line (only the exact path
+    // writes it: a workspace shared with exact calls keeps its epoch)
+    const size_t heads_bytes = kCtlBytes + (size_t)B * p.num_groups * 8;
     if (!workspace || workspace_bytes < heads_bytes)
         return set_error(STK_E_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required",
                          workspace ? workspace_bytes : (size_t)0, heads_bytes);
@@ -831,14 +882,14 @@ int stk_approx_forward(const void* X, const void* W, const float* b, float* V, i
     ga.X = X; ga.W = W; ga.bias = b; ga.B = B; ga.d = d; ga.F = F; ga.c = (int)c;
     ga.num_groups = p.num_groups; ga.tiles_per_wg = p.tpw;
     ga.cand_vals = cand_vals; ga.cand_idxs = cand_idxs;
-    ga.heads = (uint64_t*)workspace;
+    ga.heads = (uint64_t*)((unsigned char*)workspace + kCtlBytes);
     int pg = prof_begin("group_kernel", st);
     hipError_t e = launch_group(dtype, p.NB, ga, dim3((unsigned)p.nwg, (unsigned)p.nbc), st);
     prof_end(pg, st);
     if (e != hipSuccess) return hip_fail(e, "group_kernel launch");
     CandArgs ca;
     ca.cand_vals = cand_vals; ca.cand_idxs = cand_idxs;
-    ca.heads = (const uint64_t*)workspace;
+    ca.heads = (const uint64_t*)((unsigned char*)workspace + kCtlBytes);
     ca.num_groups = p.num_groups; ca.c = (int)c; ca.k = (int)k; ca.V = V; ca.I = I;
     pg = prof_begin("cand_kernel", st);
     e = launch_cand(ca, B, st);
@@ -861,6 +912,41 @@ int stk_read_probe(const void* buf, size_t bytes, uint32_t* sink, void* stream)
     const hipError_t e = launch_read_probe(buf, (int64_t)(bytes / 16), sink, ncu, st);
     prof_end(pi, st);
     if (e != hipSuccess) return hip_fail(e, "read_probe launch");
+    return 0;
+}
+
+// Test-only (not declared in include/streamtopk.h): sets the test hooks
+// (TestHooks) for later calls of every thread.  no_xch != 0 never takes the
+// threshold exchange; max_rounds >= 0 bounds the streaming kernels' retry
+// loops (-1: the default bound); xch_wait is the exchange's poll bound in
+// ticks of the 100 MHz counter (0: one poll, < 0: none).
+int stk_test_set_hooks(int no_xch, int max_rounds, int64_t xch_wait)
+{
+    clear_error();
+    std::lock_guard<std::mutex> lock(g_hooks_mu);
+    g_hooks.no_xch = no_xch;
+    g_hooks.max_rounds = max_rounds;
+    g_hooks.xch_wait = xch_wait;
+    return 0;
+}
+
+// Test-only (not declared in include/streamtopk.h): copies `bytes` between
+// host memory and the current device's no-allocation scratch at byte offset
+// `off` (write != 0: host -> scratch), synchronously, so that a test can
+// plant stale contents and read the control line.
+int stk_test_scratch_io(size_t off, void* host, size_t bytes, int write)
+{
+    clear_error();
+    if (!host || off > (size_t)STK_NOALLOC_SCRATCH_BYTES || bytes > (size_t)STK_NOALLOC_SCRATCH_BYTES - off)
+        return set_error(STK_E_INVALID, "scratch range out of bounds");
+    void* ws = nullptr;
+    int dev = 0;
+    int rc = scratch_ptr(&ws, &dev);
+    if (rc) return rc;
+    unsigned char* p = (unsigned char*)ws + off;
+    const hipError_t e = write ? hipMemcpy(p, host, bytes, hipMemcpyHostToDevice)
+                               : hipMemcpy(host, p, bytes, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpy(scratch)");
     return 0;
 }
 

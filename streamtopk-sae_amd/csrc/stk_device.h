@@ -93,15 +93,18 @@ __device__ __forceinline__ void xch_put(uint64_t* p, uint32_t tag, uint32_t data
 // Wave-level: polls n <= 64 * U words p[0..n) (U per lane) until at least
 // `need` of them carry `tag`, for at most `wait` ticks of the 100 MHz
 // real-time counter; v[u] receives the low half of word lane + 64 u if it
-// carries the tag, else 0.  Returns whether `need` words arrived (the same in
-// every lane).  wait <= 0: false at once.
+// carries the tag, else 0.  Returns how many of the n words carry the tag in
+// the last poll (>= need unless the wait ran out; the same in every lane).
+// wait == 0: one poll; wait < 0: none (every v[u] 0, returns 0).
 template <int U>
-__device__ __forceinline__ bool xch_poll(const uint64_t* p, int n, int need, uint32_t tag, int64_t wait, int lane,
-                                         uint32_t (&v)[U])
+__device__ __forceinline__ int xch_poll(const uint64_t* p, int n, int need, uint32_t tag, int64_t wait, int lane,
+                                        uint32_t (&v)[U])
 {
+    if (wait < 0) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = 0u;
-    if (wait <= 0) return false;
+        for (int u = 0; u < U; ++u) v[u] = 0u;
+        return 0;
+    }
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     for (;;) {
         int got = 0;
@@ -109,6 +112,7 @@ __device__ __forceinline__ bool xch_poll(const uint64_t* p, int n, int need, uin
         for (int u = 0; u < U; ++u) {
             const int i = lane + 64 * u;
             bool tagged = false;
+            v[u] = 0u;
             if (i < n) {
                 const uint64_t w = __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 tagged = (uint32_t)(w >> 32) == tag;
@@ -116,8 +120,7 @@ __device__ __forceinline__ bool xch_poll(const uint64_t* p, int n, int need, uin
             }
             got += __popcll(__ballot(tagged));
         }
-        if (got >= need) return true;
-        if ((int64_t)(__builtin_amdgcn_s_memrealtime() - t0) >= wait) return false;
+        if (got >= need || (int64_t)(__builtin_amdgcn_s_memrealtime() - t0) >= wait) return got;
         __builtin_amdgcn_s_sleep(1);
     }
 }
@@ -156,6 +159,16 @@ __device__ __forceinline__ uint32_t xch_kth(const uint32_t (&v)[U], int k)
         T = cnt >= k ? c : T;
     }
     return T;
+}
+
+// Partial sums stored in a workspace keep no denormal (a positive one's bits
+// could pass for an exchange tag in a word's high half): they are stored as
+// zero, a change below any fp32 score's rounding once the bias is added.
+__device__ __forceinline__ f32x4 flush_denorm4(f32x4 v)
+{
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = __builtin_fabsf(v[e]) < 1.17549435e-38f ? 0.f : v[e];
+    return v;
 }
 
 // The threshold key of score image T: the largest key below every key of

@@ -99,15 +99,47 @@ struct MainArgs {
 // least this many workgroups (an owner workgroup handles its rows one wave
 // each: at most 128 / kXchMinWg <= kMainWaves rows).
 constexpr int kXchMinWg = 16;
-// Every exact-path workspace starts with a control line (kCtlBytes): the
-// epoch (u32 at 0: calls completed on this workspace, advanced by each call's
-// merge), the exchange's count of polls that ran out (u32 at 4), the error
-// word (u64 at 8) and the running call's tag (u64 at 16).  A call's tag is
-// epoch + 1 (epoch wraps below 0xFFFFFFFF, so a tag is never 0): it differs
-// from every earlier call's on the workspace, whatever their shapes, also when
-// the call is a replay of a captured graph (whose kernel arguments never
-// change), so words that earlier calls left carry other tags.
+// Every workspace starts with a control line (kCtlBytes): the epoch (u32 at
+// 0: calls completed on this workspace, advanced by each exact call's merge),
+// the exchange's count of polls that ran out (u32 at 4), the error word (u64
+// at 8) and the running call's tag (u64 at 16).  Only the exact path's
+// kernels write it; every other buffer of every entry point (the shard
+// merge's lists, the candidate path's group heads) starts past it.
+//
+// A call's tag is epoch + 1, in [1, kTagPeriod]: the epoch runs modulo
+// kTagPeriod, so a tag is never 0 and differs from the tags of the previous
+// kTagPeriod - 1 calls on the workspace, whatever their shapes, also when the
+// call is a replay of a captured graph (whose kernel arguments never change).
+// A tag sits in the high half of a 64-bit word, and every such half any
+// kernel writes to a workspace is either a tag or outside [1, kTagPeriod]:
+//   - sort keys: the image of an fp32 score (ordered_u32), at least
+//     0x007FFFFF (-inf) for every value, or 0 (empty);
+//   - counts (lists, segments): at most 2^20, and the high half of a word
+//     only where another count is its low half, which, read as a score
+//     image, lies below every real score (a maximum or threshold that low
+//     only admits more candidates);
+//   - the sample pass's partial sums (fp32): denormals are stored as zero,
+//     so a positive one is at least 0x00800000.
+// The merge zeroes the exchange words its call used, so a tag that comes
+// round again after kTagPeriod calls meets no word of its earlier use; the
+// streaming kernel clears an error word that holds another call's tag.
 constexpr size_t kCtlBytes = 256;
+constexpr uint32_t kTagPeriod = (1u << 22) - 1;
+
+// This call's tag from the workspace's epoch (reduced modulo the period, so
+// that even a corrupted epoch yields a tag in range).
+__device__ __forceinline__ uint32_t call_tag(const uint32_t* epoch)
+{
+    return *epoch % kTagPeriod + 1u;
+}
+
+// Clears an error word that holds another call's tag (it may come round
+// again); a workgroup of this call that sets the word meanwhile keeps it.
+__device__ __forceinline__ void clear_stale_err(uint64_t* err, uint32_t tag)
+{
+    const uint64_t e = __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (e != 0ull && e != (uint64_t)tag) atomicCAS((unsigned long long*)err, (unsigned long long)e, 0ull);
+}
 
 // 500 us at the 100 MHz s_memrealtime clock: ~30x the longest wait measured
 // (the skew of the first tile's end over the grid plus two round trips,
@@ -128,8 +160,8 @@ constexpr int kCntStride = 32;
 // call then marks every row of its output (indices -1, values NaN) instead of
 // returning a silently wrong result.  A word holding another call's tag (or
 // zero) means no error: nothing has to clear it between calls.
-// STK_TEST_MAX_ROUNDS=n in the environment allows n spill rounds instead (a
-// test hook that forces that path from the host; 0: none).
+// The test-only stk_test_set_hooks(max_rounds = n) allows n spill rounds
+// instead (it forces that path from the host; 0: none).
 constexpr int kMainMaxRounds = 4096;
 constexpr int kMainLMaxRounds = 1 << 20;
 
@@ -226,7 +258,10 @@ struct MergeArgs {
                                  //   take consecutive ranks
     const uint64_t* err;         // equal to *cur (this call's tag): mark the output rows
     const uint64_t* cur;         //   (-1, NaN); both null for stk_topk_merge
-    uint32_t* epoch;             // advanced by one (workgroup 0), or null
+    uint32_t* epoch;             // advanced by one modulo kTagPeriod (workgroup 0), or null
+    uint64_t* xmax;              // the threshold exchange's words of this call, zeroed by
+    int64_t xmax_row;            //   the merge: row r's maxima xmax[r * xmax_row ..
+    uint64_t* xthr;              //   + xmax_row) and its threshold xthr[r]; null without
     float* V;
     int32_t* I;
 };
@@ -278,5 +313,7 @@ hipError_t launch_pack(const PackArgs& a, int64_t rows, hipStream_t st);
 hipError_t launch_group(int dt, int NB, const GroupArgs& a, dim3 grid, hipStream_t st);
 hipError_t launch_cand(const CandArgs& a, int64_t rows, hipStream_t st);
 hipError_t launch_read_probe(const void* buf, int64_t n16, uint32_t* sink, int ncu, hipStream_t st);
+// Zero-fills `bytes` (a multiple of 16) at 16-byte aligned `p` with a kernel (no memset node).
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t st);
 
 }  // namespace stk

@@ -203,21 +203,24 @@ __device__ __forceinline__ void xch_thresholds(const MainArgs& a, const f32x16 (
         uint32_t v[4];
         uint32_t T = 0;
         const int quorum = (3 * nwg + 3) / 4;
-        if (xch_poll<4>(xmax + (int64_t)row * nwg, nwg, a.k > quorum ? a.k : quorum, tag, a.xwait, lane, v))
-            T = xch_kth<4>(v, a.k);
-        else if (lane == 0 && a.xwait > 0)
-            atomicAdd(a.xto, 1u);
+        const int need = a.k > quorum ? a.k : quorum;
+        const int got = xch_poll<4>(xmax + (int64_t)row * nwg, nwg, need, tag, a.xwait, lane, v);
+        // any k arrived maxima bound the k-th score, a quorum or not
+        if (got >= a.k) T = xch_kth<4>(v, a.k);
+        if (got < need && lane == 0 && a.xwait > 0) atomicAdd(a.xto, 1u);
         if (lane == 0) xch_put(xthr + row, tag, T);
     }
 
-    // waves 0 and 1 poll the block's thresholds, a row per lane
+    // waves 0 and 1 poll the block's thresholds, a row per lane; a row whose
+    // threshold has not arrived when the wait runs out reads 0 (key 0:
+    // every score passes), the others keep theirs
     if (wave < 2) {
-        uint32_t v[4];
+        uint32_t v[1];
         const int base = 64 * wave;
         const int n = nrows - base < 64 ? nrows - base : 64;
-        const bool ok = n > 0 && xch_poll<4>(xthr + base, n, n, tag, a.xwait, lane, v);
-        if (n > 0 && !ok && lane == 0 && a.xwait > 0) atomicAdd(a.xto, 1u);
-        if (base + lane < BT) thr[base + lane] = xch_key(ok ? v[0] : 0u);
+        const int got = n > 0 ? xch_poll<1>(xthr + base, n, n, tag, a.xwait, lane, v) : 0;
+        if (n > 0 && got < n && lane == 0 && a.xwait > 0) atomicAdd(a.xto, 1u);
+        if (base + lane < BT) thr[base + lane] = xch_key(n > 0 ? v[0] : 0u);
     }
     __syncthreads();
 }
@@ -245,8 +248,9 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
     const int k = a.k;
     // this call's tag: the workspace's epoch (advanced by the previous call's
     // merge) + 1, recorded for this call's merge
-    const uint32_t tag = *a.epoch + 1u;
+    const uint32_t tag = call_tag(a.epoch);
     if (tid == 0) *a.cur = tag;
+    if (tid == 0 && blockIdx.x == 0 && blockIdx.y == 0) clear_stale_err(a.err, tag);
     // this workgroup's global segments: cap keys in each row's list (row
     // b0 + r at seg + r * list_cap; rows past B are never written)
     uint64_t* seg = a.list_keys + b0 * a.list_cap + a.head_span + (int64_t)blockIdx.x * cap;
@@ -387,7 +391,8 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
 // the range are staged in LDS with whole 128-byte row steps per load (X lives
 // in L2 and is read once per 64 latents).  Wave (g, sl) scores latent group g
 // (32 latents) over the range's steps sl and sl + 4; the four step lanes'
-// sums are added in a fixed order through LDS and written as whole rows.
+// sums are added in a fixed order through LDS and written as whole rows
+// (denormal sums as zero: flush_denorm4).
 // ---------------------------------------------------------------------------
 constexpr int kSampleStride = 68;   // floats per LDS-staged row of sums: 64 latents + pad (16-byte aligned)
 
@@ -507,7 +512,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a)
             const float* t0 = T + row * kSampleStride + c4;
             const f32x4 v = ((*(const f32x4*)t0 + *(const f32x4*)(t0 + WS)) + *(const f32x4*)(t0 + 2 * WS)) +
                             *(const f32x4*)(t0 + 3 * WS);
-            *(f32x4*)(Ps + j * a.p_row + ib + c4) = v;
+            *(f32x4*)(Ps + j * a.p_row + ib + c4) = flush_denorm4(v);
         }
     }
 }
@@ -698,13 +703,17 @@ __device__ __forceinline__ void merge_pass(SelSharedT<NT>& S, const uint64_t (&v
 // -1, values NaN.  The word is the same for every thread, so the whole
 // workgroup returns together.  Workgroup 0 also advances the workspace's
 // epoch for the next call (no other kernel of this call reads it; the
-// streaming kernel has recorded this call's tag in *cur).
+// streaming kernel has recorded this call's tag in *cur), and every
+// workgroup zeroes its row's threshold-exchange words.
 template <int NT = kThreads>
 __device__ __forceinline__ bool merge_marked(const MergeArgs& a, int64_t row, int tid)
 {
-    if (a.epoch != nullptr && blockIdx.x == 0 && tid == 0) {
-        const uint32_t e = *a.epoch + 1u;
-        *a.epoch = e == 0xFFFFFFFFu ? 0u : e;
+    if (a.epoch != nullptr && blockIdx.x == 0 && tid == 0) *a.epoch = (*a.epoch % kTagPeriod + 1u) % kTagPeriod;
+    if (a.xmax != nullptr) {
+        // this row's exchange words: no later call may meet them
+        uint64_t* xm = a.xmax + row * a.xmax_row;
+        for (int64_t i = tid; i < a.xmax_row; i += NT) xm[i] = 0ull;
+        if (tid == 0) a.xthr[row] = 0ull;
     }
     if (a.err == nullptr || *a.err != *a.cur) return false;
     for (int r = tid; r < a.k; r += NT) {
@@ -925,6 +934,15 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(PackArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// fill_zero_kernel: n16 16-byte words at p set to zero, grid-stride.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void fill_zero_kernel(u32x4* p, int64_t n16)
+{
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n16; i += (int64_t)gridDim.x * kThreads)
+        p[i] = u32x4{0u, 0u, 0u, 0u};
+}
+
+// ---------------------------------------------------------------------------
 // read_probe_kernel: reads n16 16-byte words once and folds them (XOR) into
 // *sink with one atomic per wave, so that no load can be elided.  The words
 // are taken as 4 KiB rows; each workgroup owns a contiguous run of rows and
@@ -1073,6 +1091,16 @@ hipError_t launch_thr(const ThrArgs& a, int64_t rows, hipStream_t st)
 hipError_t launch_read_probe(const void* buf, int64_t n16, uint32_t* sink, int ncu, hipStream_t st)
 {
     launch(read_probe_kernel, dim3((unsigned)ncu), dim3(kProbeThreads), 0, st, (const u32x4*)buf, n16, sink);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t st)
+{
+    const int64_t n16 = (int64_t)(bytes / 16);
+    int64_t wgs = (n16 + kThreads * 4 - 1) / (kThreads * 4);
+    if (wgs > 4096) wgs = 4096;
+    if (wgs < 1) wgs = 1;
+    launch(fill_zero_kernel, dim3((unsigned)wgs), dim3(kThreads), 0, st, (u32x4*)p, n16);
     return hipGetLastError();
 }
 

@@ -310,8 +310,11 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
     // this call's tag (MainArgs::epoch), recorded for this call's merge
     uint32_t tag = 0;
     if (!SAMPLE) {
-        tag = *a.epoch + 1u;
-        if (blockIdx.x == 0 && tid == 0) *a.cur = tag;
+        tag = call_tag(a.epoch);
+        if (blockIdx.x == 0 && tid == 0) {
+            *a.cur = tag;
+            clear_stale_err(a.err, tag);
+        }
         for (int i = tid; i < kLargeRows; i += kLargeThreads) {
             const int64_t row = b0 + i;
             cnt[i] = 0;
@@ -405,7 +408,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                                 f32x4 v;
 #pragma unroll
                                 for (int e = 0; e < 4; ++e) v[e] = acc[fa][n][r4 * 4 + e];
-                                *(f32x4*)(P + row * a.p_row + i) = v;
+                                *(f32x4*)(P + row * a.p_row + i) = flush_denorm4(v);
                             }
                     }
                 }
@@ -558,20 +561,22 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                     if (row >= nrows) break;
                     uint32_t v[8];
                     uint32_t T = 0;
-                    if (xch_poll<8>(xmax + (int64_t)row * nw, nw, need, tag, a.xwait, lane, v))
-                        T = xch_kth<8>(v, a.k);
-                    else if (lane == 0 && a.xwait > 0)
-                        atomicAdd(a.xto, 1u);
+                    const int got = xch_poll<8>(xmax + (int64_t)row * nw, nw, need, tag, a.xwait, lane, v);
+                    // any k arrived maxima bound the k-th score, a quorum or not
+                    if (got >= a.k) T = xch_kth<8>(v, a.k);
+                    if (got < need && lane == 0 && a.xwait > 0) atomicAdd(a.xto, 1u);
                     if (lane == 0) xch_put(xthr + row, tag, T);
                 }
-                // 3. wave w reads rows 64 w .. 64 w + 63
+                // 3. wave w reads rows 64 w .. 64 w + 63; a row whose threshold
+                //    has not arrived when the wait runs out reads 0 (every
+                //    score passes), the others keep theirs
                 {
                     uint32_t v[1];
                     const int base = 64 * wave;
                     const int n = nrows - base < 64 ? nrows - base : 64;
-                    const bool ok = n > 0 && xch_poll<1>(xthr + base, n, n, tag, a.xwait, lane, v);
-                    if (n > 0 && !ok && lane == 0 && a.xwait > 0) atomicAdd(a.xto, 1u);
-                    thr[base + lane] = xch_key(ok ? v[0] : 0u);
+                    const int got = n > 0 ? xch_poll<1>(xthr + base, n, n, tag, a.xwait, lane, v) : 0;
+                    if (n > 0 && got < n && lane == 0 && a.xwait > 0) atomicAdd(a.xto, 1u);
+                    thr[base + lane] = xch_key(n > 0 ? v[0] : 0u);
                 }
                 __syncthreads();
             }

@@ -42,6 +42,13 @@ SIGNATURES = {
                                 ctypes.POINTER(ctypes.c_int64)]),
 }
 
+# Test-only exports (not declared in include/streamtopk.h): hooks that force
+# paths real inputs never take, and a window on the no-allocation scratch.
+TEST_SIGNATURES = {
+    "stk_test_set_hooks": (_int, [_int, _int, _i64]),
+    "stk_test_scratch_io": (_int, [ctypes.c_size_t, _vp, ctypes.c_size_t, _int]),
+}
+
 _lock = threading.Lock()
 _lib = None
 
@@ -58,7 +65,7 @@ def load():
                     "libstreamtopk_hip.so not built (expected at %s). Run: "
                     "make -C streamtopk-sae_amd  (or __graft_entry__.build())" % LIB_PATH)
             lib = ctypes.CDLL(LIB_PATH)
-            for name, (res, args) in SIGNATURES.items():
+            for name, (res, args) in list(SIGNATURES.items()) + list(TEST_SIGNATURES.items()):
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args

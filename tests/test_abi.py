@@ -115,10 +115,11 @@ def test_shard_offset_errors(f_offset, F, msg):
 def test_merge_workspace_and_errors():
     lib = _lib.load()
     nb = ctypes.c_size_t(0)
-    # dense candidate lists of nparts*k keys per row (256-byte aligned), then one
-    # 128-byte count line per row
+    # the 256-byte control line (left to the exact path), dense candidate
+    # lists of nparts*k keys per row (256-byte aligned), then one 128-byte
+    # count line per row
     assert lib.stk_topk_merge_workspace_bytes(4, 8, 3, ctypes.byref(nb)) == 0
-    assert nb.value == 4 * 24 * 8 + 4 * 32 * 4
+    assert nb.value == 256 + 4 * 24 * 8 + 4 * 32 * 4
     assert lib.stk_topk_merge_workspace_bytes(0, 8, 3, ctypes.byref(nb)) == 0 and nb.value == 0
     for B, k, nparts, msg in [(4, 3, 2, "unsupported k=3"), (4, 8, 0, "nparts=0 out of range"),
                               (4, 128, 9000, "nparts=9000 out of range")]:

@@ -20,7 +20,7 @@ import pytest
 import torch
 
 import oracle
-from parity import check_against_scores
+from parity import check_against_scores, term_magnitudes
 from streamtopk_sae import make_inputs, recall_at_k, topk_sae_cuda_approx, topk_sae_cuda_exact
 
 pytestmark = pytest.mark.gpu
@@ -32,23 +32,27 @@ def _np(t):
     return t.detach().float().cpu().numpy()
 
 
-def _scores_f64(X, W, b, chunk=1 << 16):
-    """float64 scores X @ W.T + b on the GPU, F-chunk by F-chunk, as a host array."""
+def _scores_f64(X, W, b, chunk=1 << 16, magnitudes=False):
+    """float64 scores X @ W.T + b on the GPU, F-chunk by F-chunk, as a host
+    array; with magnitudes, also |X| @ |W|.T + |b| (parity.term_magnitudes)."""
     out = np.empty((X.shape[0], W.shape[0]), dtype=np.float64)
+    mag = np.empty_like(out) if magnitudes else None
     Xd = X.double()
     for f0 in range(0, W.shape[0], chunk):
         f1 = min(W.shape[0], f0 + chunk)
         out[:, f0:f1] = (Xd @ W[f0:f1].double().T + b[f0:f1].double()).cpu().numpy()
-    return out
+        if magnitudes:
+            mag[:, f0:f1] = term_magnitudes(X, W[f0:f1], b[f0:f1])
+    return (out, mag) if magnitudes else out
 
 
 @pytest.fixture(scope="module")
 def c3(cuda_dev):
     print("case config3 inputs", flush=True)
     X, W, b = make_inputs(C3["B"], C3["d"], C3["F"], torch.bfloat16, seed=0, device=cuda_dev)
-    S = _scores_f64(X, W, b)
+    S, A = _scores_f64(X, W, b, magnitudes=True)
     exact = {k: topk_sae_cuda_exact(X, W, b, k) for k in (16, 32)}
-    return X, W, b, S, exact
+    return X, W, b, S, A, exact
 
 
 def _k_of(c):
@@ -58,11 +62,12 @@ def _k_of(c):
 
 @pytest.mark.parametrize("c", [16, 32, 64, 128])
 def test_config3_default_path(c3, c):
-    X, W, b, S, exact = c3
+    X, W, b, S, A, exact = c3
     k = _k_of(c)
     print(f"case config3 default c={c} k={k}", flush=True)
     V, I = topk_sae_cuda_approx(X, W, b, k, c)
-    ties = check_against_scores(V.cpu().numpy(), I.cpu().numpy(), S, k, 2e-3, f"config3 c={c}")
+    ties = check_against_scores(V.cpu().numpy(), I.cpu().numpy(), S, k, 2e-3, f"config3 c={c}",
+                                A=A, d=C3["d"], max_tie_frac=0.02)
     if ties:
         print(f"[ties] config3 c={c}: {ties} row(s)")
     # k <= c: the union of the per-group top-c holds the exact top-k
@@ -71,13 +76,18 @@ def test_config3_default_path(c3, c):
     assert recall_at_k(I, Ie) == 1.0
 
 
-def _check_group_candidates(cv, ci, S_row, c, tol, name):
+def _check_group_candidates(cv, ci, S_row, c, tol, name, A_row=None, d=None):
     """One row's (G, c) candidates against its float64 scores: each group's
-    top-c (value descending, near-ties allowed), padded past F."""
+    top-c (value descending, near-ties allowed), padded past F; with A_row,
+    values held to the fp32 accumulation bound."""
     G = cv.shape[0]
     F = S_row.size
     Sg = np.full((G, 128), -np.inf)
     Sg.reshape(-1)[:F] = S_row
+    Ag = None
+    if A_row is not None:
+        Ag = np.zeros((G, 128))
+        Ag.reshape(-1)[:F] = A_row
     assert np.all(np.diff(cv, axis=1) <= 0), f"{name}: candidates not descending"
     real = ci >= 0
     assert np.all(cv[~real] == np.float32(-3.402823466e38)), f"{name}: padding value"
@@ -87,18 +97,20 @@ def _check_group_candidates(cv, ci, S_row, c, tol, name):
     assert np.all(g_of == np.arange(G)[:, None]), f"{name}: candidate outside its group"
     full = n_real >= c
     local = np.where(real, ci - 128 * np.arange(G)[:, None], 0)
-    return check_against_scores(cv[full], local[full], Sg[full], c, tol, name)
+    return check_against_scores(cv[full], local[full], Sg[full], c, tol, name,
+                                A=None if Ag is None else Ag[full], d=d)
 
 
 @pytest.mark.parametrize("c", [16, 32, 64, 128])
 def test_config3_candidate_buffer(c3, c):
-    X, W, b, S, exact = c3
+    X, W, b, S, A, exact = c3
     k = _k_of(c)
     G = C3["F"] // 128
     print(f"case config3 candidates c={c} k={k}", flush=True)
     cb = torch.empty((C3["B"], G, c), dtype=torch.float32, device=X.device)
     V, I = topk_sae_cuda_approx(X, W, b, k, c, candidate_buffer=cb)
-    check_against_scores(V.cpu().numpy(), I.cpu().numpy(), S, k, 2e-3, f"config3 cand c={c}")
+    check_against_scores(V.cpu().numpy(), I.cpu().numpy(), S, k, 2e-3, f"config3 cand c={c}",
+                         A=A, d=C3["d"], max_tie_frac=0.02)
     # the same latents as the exact kernel; values to fp32 rounding (the exact
     # path scores its sampled latents in d ranges, summed in another order)
     # (a latent tied with the k-th to within that rounding may trade places)
@@ -112,7 +124,8 @@ def test_config3_candidate_buffer(c3, c):
     assert torch.equal(cv, cb)
     cvn, cin = cv.cpu().numpy(), ci.cpu().numpy()
     for r in (0, 61, 127):
-        ties = _check_group_candidates(cvn[r], cin[r], S[r], c, 2e-3, f"config3 c={c} row {r}")
+        ties = _check_group_candidates(cvn[r], cin[r], S[r], c, 2e-3, f"config3 c={c} row {r}",
+                                       A_row=A[r], d=C3["d"])
         if ties:
             print(f"[ties] config3 c={c} row {r}: {ties} group(s)")
 
@@ -121,7 +134,7 @@ def test_config3_recall_per_c(c3):
     """recall@k of the approximate op against the exact kernel for every c
     (run_recall.py:77-92 statistics): non-decreasing in c, and 1 because
     k <= c (reference test_recall.py:22-96 asks for > 0.9 at c=128)."""
-    X, W, b, S, exact = c3
+    X, W, b, S, A, exact = c3
     rec = []
     for c in (16, 32, 64, 128):
         k = _k_of(c)
@@ -151,8 +164,9 @@ def test_large_batch_b2048(cuda_dev):
     print("case B=2048 d=768 F=131072 k=32", flush=True)
     X, W, b = make_inputs(2048, 768, 131072, torch.bfloat16, seed=5, device=cuda_dev)
     V, I = topk_sae_cuda_exact(X, W, b, 32)
-    S = _scores_f64(X, W, b)
-    ties = check_against_scores(V.cpu().numpy(), I.cpu().numpy(), S, 32, 2e-3, "B=2048")
+    S, A = _scores_f64(X, W, b, magnitudes=True)
+    ties = check_against_scores(V.cpu().numpy(), I.cpu().numpy(), S, 32, 2e-3, "B=2048",
+                                A=A, d=768, max_tie_frac=0.02)
     if ties:
         print(f"[ties] B=2048: {ties} row(s)")
 

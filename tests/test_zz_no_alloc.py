@@ -7,6 +7,7 @@ oracle scores at the bf16 tolerance.  A problem larger than the scratch is
 rejected before any device work."""
 import ctypes
 
+import numpy as np
 import pytest
 import torch
 
@@ -111,3 +112,59 @@ def test_noalloc_graph_replays(cuda_dev):
         torch.cuda.synchronize()
         assert torch.equal(Vg, Vw) and torch.equal(Ig, Iw), f"replay {i} differs from stk_exact_forward"
         assert torch.equal(Ve, Vw) and torch.equal(Ie, Iw), f"eager call after replay {i} differs"
+
+
+TAG_PERIOD = (1 << 22) - 1   # kTagPeriod: tags run 1 .. TAG_PERIOD
+IMG_100 = 0xC2C80000         # ordered_u32(100.0f): a stale sort key's high word
+
+
+def _scratch_io(off, arr, write):
+    lib = _lib.load()
+    buf = np.ascontiguousarray(arr)
+    _lib.check(lib.stk_test_scratch_io(off, buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes, int(write)))
+    return buf
+
+
+def _epoch():
+    torch.cuda.synchronize()
+    return int(_scratch_io(0, np.zeros(1, dtype=np.uint32), False)[0])
+
+
+def _set_epoch(e):
+    torch.cuda.synchronize()
+    _scratch_io(0, np.array([e], dtype=np.uint32), True)
+
+
+def _plant_stale_keys(nbytes=32 << 20):
+    """The scratch past its control line full of sort keys of score 100."""
+    torch.cuda.synchronize()
+    j = np.arange(nbytes // 8, dtype=np.uint64)
+    keys = (np.uint64(IMG_100) << np.uint64(32)) | (np.uint64(0xFFFFFFFF) - j)
+    _scratch_io(256, keys, True)
+
+
+@pytest.mark.parametrize("B,d,F,k", [(128, 256, 65536, 32), (600, 128, 81920, 64)])
+def test_noalloc_preset_epoch_and_wrapped_tag(cuda_dev, B, d, F, k):
+    """The static scratch keeps what earlier calls left.  Planted stale sort
+    keys under an epoch preset to one below their high word (a tag taken
+    straight from it would match them), then a tag that comes round again
+    (the epoch set back) on inputs with 1000x smaller scores: every result
+    equals stk_exact_forward's on a fresh workspace, bit for bit, and the
+    oracle's."""
+    print(f"case noalloc preset epoch B={B} d={d} F={F} k={k}", flush=True)
+    X, W, b = make_inputs(B, d, F, torch.bfloat16, seed=70, device=cuda_dev)
+    _no_alloc(X, W, b, k)
+    cases = [("stale keys, epoch below their word", IMG_100 - 1, X, True),
+             ("tag 6, first use", 5, X, False),
+             ("tag 6 again, scores 1000x smaller", 5, X * 1e-3, False)]
+    for name, epoch, Xc, plant in cases:
+        if plant:
+            _plant_stale_keys()
+        _set_epoch(epoch)
+        Vn, In = _no_alloc(Xc, W, b, k)
+        Vw, Iw = _with_workspace(Xc, W, b, k)
+        torch.cuda.synchronize()
+        assert torch.equal(Vn, Vw) and torch.equal(In, Iw), name
+        S = (Xc.double() @ W.double().T + b.double()).cpu().numpy()
+        check_against_scores(Vn.cpu().numpy(), In.cpu().numpy(), S, k, 2e-3, f"noalloc {name}")
+        assert _epoch() < TAG_PERIOD
