@@ -19,6 +19,19 @@ def baseline_eager(X, W_enc, b_enc, k):
     return values, indices.to(torch.int32)
 
 
+def gaussian_inputs(B, d, F, dtype, seed=0, device="cuda"):
+    """The reference harness's gaussian inputs (streamtopk_sae/utils.py:50-54,
+    its STREAMTOPK_DATA=gaussian branch): X and W_enc drawn N(0, 1) directly in
+    `dtype` from one seeded CPU generator (W_enc rows not normalised), b_enc
+    zero."""
+    rng = torch.Generator()
+    rng.manual_seed(seed)
+    X = torch.randn(B, d, dtype=dtype, generator=rng)
+    W = torch.randn(F, d, dtype=dtype, generator=rng)
+    b = torch.zeros(F, dtype=torch.float32)
+    return X.to(device), W.to(device), b.to(device)
+
+
 # impl name -> fn(X, W, b, k); cuda_approx uses c = max(16, k) as the reference does
 IMPL_FNS = {
     "eager": baseline_eager,

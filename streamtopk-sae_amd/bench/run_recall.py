@@ -4,7 +4,18 @@
 c = k * c_multiplier snapped to the nearest supported c (ties to the smaller),
 then raised to the smallest supported c >= k.  Per-row recall |pred & true| / k.
 
+--oracle picks the dense reference the recall is scored against:
+  upcast   the scores of the upcast fp32 inputs (streamtopk_sae.reference, the
+           quantity the kernels compute; default);
+  rounded  the reference's own formula (reference.py:17): the matmul in the
+           input dtype, so bf16/fp16 scores are rounded before the fp32 bias
+           is added and top-k picks among the rounded values.
+--data picks the inputs: ours (streamtopk_sae.inputs.make_inputs, unit-norm
+W_enc rows, b_enc ~ N(0, 0.1^2)) or gaussian (the reference harness's gaussian
+branch, bench.common.gaussian_inputs: X, W_enc ~ N(0, 1), b_enc = 0).
+
   python -m bench.run_recall --out results/recall.csv
+  python -m bench.run_recall --oracle rounded --data gaussian --B 128 --d 2048
   python -m bench.run_recall --dry-run
 """
 import numpy as np
@@ -32,7 +43,11 @@ def snap_c(k, c_mult):
 def main(argv=None):
     parser = common.new_parser(__doc__, "results/recall.csv")
     common.add_grid_filters(parser)
+    parser.add_argument("--oracle", choices=["upcast", "rounded"], default="upcast")
+    parser.add_argument("--data", choices=["ours", "gaussian"], default="ours")
     args = parser.parse_args(argv)
+    oracle = reference_topk_sae if args.oracle == "upcast" else common.baseline_eager
+    gen = make_inputs if args.data == "ours" else common.gaussian_inputs
     cells = [dry_run_cell(RECALL_GRID)] if args.dry_run else list(filter_cells(iter_grid(RECALL_GRID), args))
     rows = []
     for cell in cells:
@@ -40,8 +55,8 @@ def main(argv=None):
         c = snap_c(k, cm)
         key = {"B": B, "d": d, "F": F, "k": k, "c": c, "c_multiplier": cm, "dtype": dt}
         try:
-            X, W, b = make_inputs(B, d, F, dtype=str_to_dtype(dt), device="cuda")
-            _, ref_i = reference_topk_sae(X, W, b, k)
+            X, W, b = gen(B, d, F, dtype=str_to_dtype(dt), device="cuda")
+            _, ref_i = oracle(X, W, b, k)
             _, pred_i = topk_sae_cuda_approx(X, W, b, k, c)
             r = recall_per_row(pred_i, ref_i).numpy()
             row = {**key, "recall_mean": float(np.mean(r)), "recall_std": float(np.std(r)),

@@ -144,6 +144,37 @@ def test_recall_csv(cuda_dev, tmp_path):
 
 
 @pytest.mark.gpu
+def test_recall_rounded_oracle_gaussian(cuda_dev, tmp_path):
+    """The reference's published recall setting: its gaussian inputs (X, W_enc
+    ~ N(0, 1) in bf16, b_enc = 0) scored against its own dense formula, which
+    rounds the bf16 scores (|score| ~ 200 here, a bf16 step of 1.0) before
+    top-k.  The approximate op returns the exact fp32 top-k, so its recall
+    against that oracle is the exact op's, below 1 where the rounding ties or
+    reorders latents near the k-th score."""
+    import torch
+    out = tmp_path / "recall.csv"
+    run_script("run_recall", "--B", "128", "--d", "2048", "--F", "262144", "--k", "32", "--oracle", "rounded",
+               "--data", "gaussian", "--out", str(out))
+    fields, rows = read_csv(out)
+    assert fields == RECALL_FIELDS
+    assert all(r["status"] == "ok" for r in rows)
+    rec = {float(r["recall_mean"]) for r in rows}
+    assert len(rec) == 1   # the same latents for every c (k <= c)
+    from streamtopk_sae import recall_at_k, topk_sae_cuda_exact
+    # the same inputs (bench.common.gaussian_inputs, seed 0) and oracle
+    # (bench.common.baseline_eager) in this process
+    rng = torch.Generator()
+    rng.manual_seed(0)
+    X = torch.randn(128, 2048, dtype=torch.bfloat16, generator=rng).to(cuda_dev)
+    W = torch.randn(262144, 2048, dtype=torch.bfloat16, generator=rng).to(cuda_dev)
+    b = torch.zeros(262144, dtype=torch.float32, device=cuda_dev)
+    _, I_ex = topk_sae_cuda_exact(X, W, b, 32)
+    I_rd = torch.topk((X @ W.T + b).float(), 32, dim=-1).indices
+    assert float(rows[0]["recall_mean"]) == pytest.approx(recall_at_k(I_ex, I_rd), abs=1e-9)
+    assert float(rows[0]["recall_mean"]) < 1.0
+
+
+@pytest.mark.gpu
 def test_memory_gpu_cells(cuda_dev, tmp_path):
     out = tmp_path / "memory.csv"
     # at the headline F the (B, F) fp32 scores (134 MB) outweigh the streaming

@@ -47,9 +47,15 @@ def _kernel(asm, dt, sample):
 
 
 def _loop_blocks(body):
-    """Basic blocks of the kernel that issue MFMAs (the d-step loop)."""
+    """The d-steps: each basic block of the kernel that issues MFMAs, from its
+    first MFMA to its last (the tile's last step shares its block with the
+    start of the epilogue, whose branches are not part of the d-step)."""
     blocks = re.split(r"\n(?=\.LBB\d+_\d+:)", body)
-    return [b for b in blocks if "v_mfma" in b]
+    out = []
+    for b in blocks:
+        if "v_mfma" in b:
+            out.append(b[b.index("v_mfma"):b.rindex("v_mfma")])
+    return out
 
 
 @pytest.mark.parametrize("dt", [0, 1, 2])
