@@ -539,14 +539,14 @@ struct TileStream {
         set_rows(0);
         u32x4 w0[kWChunks], w1[kWChunks];
         u32x4 x0[kXChunks], x1[kXChunks];
-        if (wave == 0) {
-            float bn[kTileF / 64];
-            bias_load(bn, 0);
-            bias_store(bn, bias_lds);
-        }
+        // the first two steps' loads go out first; wave 0's bias loads after
+        // them, so that neither waits for the other's round trip
         issue(x0, w0);
         issue(x1, w1);
+        float bn0[kTileF / 64];
+        if (wave == 0) bias_load(bn0, 0);
         store(x0, w0, xs0, ws0);
+        if (wave == 0) bias_store(bn0, bias_lds);
         issue(x0, w0);
         __syncthreads();
         acc_reset(acc, bias_lds, kBiasInit);

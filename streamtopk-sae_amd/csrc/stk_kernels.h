@@ -133,6 +133,20 @@ __device__ __forceinline__ uint32_t call_tag(const uint32_t* epoch)
     return *epoch % kTagPeriod + 1u;
 }
 
+// The epoch as a vector load, for kernels that need the tag only after
+// their first tile: issued at the start, it overlaps the first loads of W
+// instead of stalling the first wait on the scalar counter, which every
+// kernel-argument load shares.  call_tag_of turns it into the tag.
+__device__ __forceinline__ uint32_t load_epoch(const uint32_t* epoch)
+{
+    return __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint32_t call_tag_of(uint32_t epoch)
+{
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)(epoch % kTagPeriod + 1u));
+}
+
 // Clears an error word that holds another call's tag (it may come round
 // again); a workgroup of this call that sets the word meanwhile keeps it.
 __device__ __forceinline__ void clear_stale_err(uint64_t* err, uint32_t tag)

@@ -247,10 +247,9 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
     const int64_t B = a.B, F = a.F;
     const int k = a.k;
     // this call's tag: the workspace's epoch (advanced by the previous call's
-    // merge) + 1, recorded for this call's merge
-    const uint32_t tag = call_tag(a.epoch);
-    if (tid == 0) *a.cur = tag;
-    if (tid == 0 && blockIdx.x == 0 && blockIdx.y == 0) clear_stale_err(a.err, tag);
+    // merge) + 1, recorded for this call's merge after the first tile (the
+    // epoch's load overlaps the first tile's)
+    const uint32_t epoch = load_epoch(a.epoch);
     // this workgroup's global segments: cap keys in each row's list (row
     // b0 + r at seg + r * list_cap; rows past B are never written)
     uint64_t* seg = a.list_keys + b0 * a.list_cap + a.head_span + (int64_t)blockIdx.x * cap;
@@ -283,7 +282,13 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
 
     f32x16 acc[NB];
     // the accumulators start at the bias: ac holds the scores at the epilogue
+    uint32_t tag = 0;
     ts.template run<true>(acc, smem, bias_lds, [&](int t, f32x16 (&ac)[NB], const float (&)[16]) {
+        if (t == 0) {
+            tag = call_tag_of(epoch);
+            if (tid == 0) *a.cur = tag;
+            if (tid == 0 && blockIdx.x == 0 && blockIdx.y == 0) clear_stale_err(a.err, tag);
+        }
         // latent of accumulator register r of this lane: fl + 8*(r/4) + r%4
         const int64_t tile0 = (ts.tile_begin + t) * (int64_t)kTileLatents;
         const int64_t fl = tile0 + wave * 32 + h * 4;
