@@ -2,25 +2,25 @@
 //
 // mainl_kernel: one workgroup of 4 waves (one per SIMD, up to 512 registers
 // each) owns 256 rows and a contiguous range of 256-latent tiles.  The waves
-// form a 2 x 2 grid: each scores 128 latents x 128 rows per tile as 4 x 4
-// blocks of v_mfma_f32_32x32x16, with the 256 accumulators per lane in AGPRs.
-// Both operands come from LDS; each 16-byte operand read feeds 4 MFMAs.
+// form a 2 x 2 grid: each scores 128 latents x 128 rows per tile as 8 x 8
+// blocks of v_mfma_f32_16x16x32, with the 256 accumulators per lane in AGPRs.
+// Both operands come from LDS; each 16-byte operand read feeds 8 MFMAs.
 //   - W and X: whole 128-byte lines loaded straight from global memory into
 //     2-stage LDS rings (buffer loads with the lds flag: no staging
 //     registers, no LDS-store instructions), one d-step ahead; 128-byte rows
 //     with the 16-byte chunks swizzled, so the MFMA-layout reads hit no bank
 //     conflicts.  One barrier per d-step.  The W lines are shared through L2
 //     by the row blocks of the W range.
-//   - The next step's LDS loads are spread through the first two quads'
-//     MFMAs (one per MFMA), not issued as a burst: with one wave per SIMD, a
-//     vector-memory instruction that cannot issue stalls the MFMAs behind it.
+//   - The next step's LDS loads are spread through the MFMAs (one per MFMA),
+//     not issued as a burst: with one wave per SIMD, a vector-memory
+//     instruction that cannot issue stalls the MFMAs behind it.
 //   - The pipeline restarts at every tile, so the epilogue holds no prefetch.
 //   - bias: the tile's 256 values are loaded at the tile start and staged in
 //     LDS for the epilogue.
-//   - epilogue, one row block at a time and no barrier between blocks: the
-//     accumulators are read once, biased, compared with the row threshold
-//     and staged in LDS; each lane reserves its survivors' slots in the row's
-//     queue segment in global memory (counters in LDS), and the wave's
+//   - epilogue, two 16-row blocks at a time and no barrier between them: the
+//     accumulators are read once, biased, compared with the row thresholds
+//     and staged in LDS; each lane reserves its survivors' slots in the rows'
+//     queue segments in global memory (counters in LDS), and the wave's
 //     survivors are spread over its lanes for the stores.  Survivors that
 //     find a segment full wait for one barrier per tile; then the full
 //     segments are rank-compacted to their top-k, which raises the row
@@ -46,12 +46,13 @@ namespace {
 
 constexpr int kLWaves = 4;
 // The waves form a 2 x 2 grid over the 256 x 256 tile: wave w scores latents
-// (w & 1) * 128 .. +127 for rows (w >> 1) * 128 .. +127, as 4 x 4 blocks of
-// 32 x 32.  Each operand block read from LDS feeds 4 MFMAs.
-constexpr int kLNB = 4;                      // 32-row blocks per wave
-constexpr int kLFrags = 4;                   // 32-latent fragments per wave
+// (w & 1) * 128 .. +127 for rows (w >> 1) * 128 .. +127, as 8 x 8 blocks of
+// 16 x 16.  Each operand block read from LDS feeds 8 MFMAs.
+constexpr int kLNB = 8;                      // 16-row blocks per wave
+constexpr int kLLat = 8;                     // 16-latent blocks per wave
+constexpr int kLPairs = kLNB / 2;            // epilogue rounds: two row blocks each
 constexpr int kLTile = 256;                  // latents per tile
-static_assert(2 * 32 * kLFrags == kLTile && 2 * 32 * kLNB == kLargeRows, "2 x 2 wave grid");
+static_assert(2 * 16 * kLLat == kLTile && 2 * 16 * kLNB == kLargeRows, "2 x 2 wave grid");
 constexpr int kLWChunks = kLTile * 8 / kLargeThreads;       // 16-byte W chunks per thread per d-step
 constexpr int kLWStage = kLTile * kStepBytes;               // W ring stage: 256 rows x 128 B (swizzled)
 constexpr int kLXStage = kLargeRows * kStepBytes;           // X ring stage: 256 rows x 128 B (swizzled)
@@ -70,7 +71,46 @@ __device__ __forceinline__ void static_for(Fn&& f)
     }
 }
 
-template <int DT, bool SAMPLE>
+// One 16 x 16 block through the k = 32 MFMA (fp16/bf16), or element e of
+// the operands through the k = 4 one (fp32), accumulating into acc in place.
+// Lane l supplies A[l % 16][8 (l / 16) + e'] in a and B[8 (l / 16) + e'][l % 16]
+// in b (fp32: 4 (l / 16) + e'), e' over the 16 bytes; register r of lane l
+// receives D[4 (l / 16) + r][l % 16].  On MI355X this form sustains ~12 % more
+// FLOP/s than the 32x32 one under the power limit (1.99-2.01 against
+// 1.73-1.81 PF/s in an MFMA loop on random operands): the same products with
+// half the accumulator traffic per product.
+// Written as volatile asm with the accumulator tied to
+// its AGPRs: through the builtin, the compiler gives each of the 64 4-register
+// accumulators a new register per MFMA and copies them back around every
+// d-step (hundreds of AGPR/VGPR moves and spills per step), and volatile
+// keeps the MFMAs in program order with the reads and loads woven between
+// them.  The compiler's hazard checks do not look inside the asm: the
+// operands are only ever written by LDS reads (whose waits the compiler
+// counts), an MFMA's accumulator is next read by an MFMA 64 MFMAs later,
+// the zeros written into the accumulators at a tile's start are separated
+// from its first MFMA by the tile's first loads, barrier and operand reads
+// (2 wait states needed), and the reads of the results wait for mfma_drain.
+template <int DT>
+__device__ __forceinline__ void mfma16_tied(f32x4& acc, const u32x4& a, const u32x4& b, int e)
+{
+    if constexpr (DT == DT_BF16)
+        asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+    else if constexpr (DT == DT_F16)
+        asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+    else
+        asm volatile("v_mfma_f32_16x16x4_f32 %0, %1, %2, %0" : "+a"(acc) : "v"(a[e]), "v"(b[e]));
+}
+
+// Wait states between the last MFMA of a tile and the first read of its
+// results (a VALU read of an MFMA result needs up to passes + 4 = 20 on
+// gfx950; 3 x 8 here).  Volatile, so that it stays between the MFMAs and the
+// (volatile) accumulator reads.
+__device__ __forceinline__ void mfma_drain()
+{
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+}
+
+template <int DT, bool SAMPLE, bool TAILK>
 struct BigStream {
     const unsigned char* W;
     int64_t row_bytes;           // bytes of a W row and of an X row (d elements)
@@ -81,14 +121,14 @@ struct BigStream {
     int tail;                    // elements of d in the last d-step when it is partial, else 0
     int s_lo, s_hi;              // d-steps [s_lo, s_hi) of every tile
     int samp_log2;               // SAMPLE: tile t covers sampled latents t*256 ..
-    int tid, lane, wave, h, jl;
+    int tid, lane, wave;
 
     // load cursors (absolute d-steps), uniform
     int ws, xs;
     __amdgpu_buffer_rsrc_t wres, xres, zres;      // wres: this wave's 64-row run of the tile
     int wvoff[kLWChunks];        // W LDS load i of this wave: this lane's source offset in the wave's run
     int xvoff[kLXChunks];        // X LDS load i of this wave: this lane's source offset in the row block
-    int xrd[4];                  // X operand read offset of quad q (row jl of block 0)
+    int rd[2];                   // operand read offset of MFMA step m (row lane % 16 of block 0)
 
     __device__ __forceinline__ void init()
     {
@@ -101,8 +141,11 @@ struct BigStream {
             wvoff[i] = r * (int)row_bytes + (((lane & 7) ^ xswz(r)) * 16);
             xvoff[i] = (wave * 64 + r) * (int)row_bytes + (((lane & 7) ^ xswz(r)) * 16);
         }
+        // lanes 16 g .. 16 g + 15 of MFMA step m read chunk 4 m + g of rows
+        // 0 .. 15 of a block (rows 16 j + i share swizzle xswz(i))
+        const int i = lane & 15, g = lane >> 4;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) xrd[q] = jl * kStepBytes + (((h * 4 + q) ^ xswz(jl)) * 16);
+        for (int m = 0; m < 2; ++m) rd[m] = i * kStepBytes + (((4 * m + g) ^ xswz(i)) * 16);
         const int64_t nrows = (B - b0 < kLargeRows) ? B - b0 : kLargeRows;
         xres = make_rsrc(X + b0 * row_bytes, nrows * row_bytes);
         zres = make_rsrc(X, 0);
@@ -171,63 +214,61 @@ struct BigStream {
         ++xs;
     }
 
-    // One d-step from LDS stages wst / xst, with the next step's LDS loads
-    // folded into the MFMA stream: W(s+1) into wnx during quad 0 and X(s+1)
-    // into xnx during quad 1, one load instruction between MFMAs, so that the
-    // texture path works in the background instead of stalling the wave's
-    // in-order issue.  Each quad also reads the 8 operand blocks (4 W
-    // fragments, 4 X blocks) of the next.
-    __device__ __forceinline__ void step(f32x16 (&acc)[kLFrags][kLNB], const unsigned char* wst,
+    // One d-step from LDS stages wst / xst: two MFMA phases m of k = 32 (half
+    // the step's d each), 64 MFMAs apiece (fp32: 4 x 64 of k = 4, one element
+    // of the 16-byte operands per round of 64).  The operands of phase 0 are
+    // read up front; phase 1's are read during phase 0's MFMAs, one read
+    // between MFMAs.  The next d-step's LDS loads are folded into the MFMA
+    // stream too -- W(s+1) into wnx during phase 0, X(s+1) into xnx during
+    // phase 1, one load instruction between MFMAs -- so that the texture path
+    // works in the background instead of stalling the wave's in-order issue.
+    // The MFMAs are volatile asm (mfma16_tied), so this program order is the
+    // issue order.
+    __device__ __forceinline__ void step(f32x4 (&acc)[kLLat][kLNB], const unsigned char* wst,
                                          const unsigned char* xst, unsigned char* wnx, unsigned char* xnx)
     {
-        const unsigned char* wl = wst + (wave & 1) * (32 * kLFrags) * kStepBytes;
-        const unsigned char* xl = xst + (wave >> 1) * (32 * kLNB) * kStepBytes;
-        u32x4 bA[kLNB], bB[kLNB], aA[kLFrags], aB[kLFrags];
-#pragma unroll
-        for (int n = 0; n < kLNB; ++n) bA[n] = *(const u32x4*)(xl + xrd[0] + (32 * n) * kStepBytes);
-#pragma unroll
-        for (int fa = 0; fa < kLFrags; ++fa) aA[fa] = *(const u32x4*)(wl + xrd[0] + (32 * fa) * kStepBytes);
-        __builtin_amdgcn_sched_barrier(0);   // quad 0's operands are all in flight before any MFMA
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            u32x4 (&cur)[kLNB] = (q & 1) ? bB : bA;
-            u32x4 (&nxt)[kLNB] = (q & 1) ? bA : bB;
-            u32x4 (&wc)[kLFrags] = (q & 1) ? aB : aA;
-            u32x4 (&wn)[kLFrags] = (q & 1) ? aA : aB;
-            if (q < 3) {
-#pragma unroll
-                for (int fa = 0; fa < kLFrags; ++fa)
-                    wn[fa] = *(const u32x4*)(wl + xrd[q + 1] + (32 * fa) * kStepBytes);
-#pragma unroll
-                for (int n = 0; n < kLNB; ++n) nxt[n] = *(const u32x4*)(xl + xrd[q + 1] + (32 * n) * kStepBytes);
+        const unsigned char* wl = wst + (wave & 1) * (16 * kLLat) * kStepBytes;
+        const unsigned char* xl = xst + (wave >> 1) * (16 * kLNB) * kStepBytes;
+        const int w = __builtin_amdgcn_readfirstlane(ws);   // the next d-step (ws == xs)
+        const bool live = w < s_hi;
+        const __amdgpu_buffer_rsrc_t wr = live ? wres : zres, xr = live ? xres : zres;
+        const int so = live ? w * kStepBytes : 0;
+        // the next d-step is the partial last one (only kernels built for a
+        // partial last step look)
+        const bool tl = TAILK && w == nds - 1;
+        u32x4 a0[kLLat], b0[kLNB], a1[kLLat], b1[kLNB];
+        // operand read r of a phase, in first-use order: W block 0, the X
+        // blocks, W blocks 1 .. 7
+        auto rd_op = [&](u32x4 (&av)[kLLat], u32x4 (&bv)[kLNB], int m, auto rc) {
+            constexpr int r = decltype(rc)::value;
+            if constexpr (r == 0) av[0] = *(const u32x4*)(wl + rd[m]);
+            else if constexpr (r <= kLNB) bv[r - 1] = *(const u32x4*)(xl + rd[m] + (16 * (r - 1)) * kStepBytes);
+            else av[r - kLNB] = *(const u32x4*)(wl + rd[m] + (16 * (r - kLNB)) * kStepBytes);
+        };
+        static_for<kLLat + kLNB>([&](auto rc) { rd_op(a0, b0, 0, rc); });
+        constexpr int E = DT == DT_F32 ? 4 : 1;   // MFMA rounds per phase
+        // phase 0: (MFMA, DS read) x 16, (MFMA, W load) x 8, MFMA x the rest
+        static_for<E * kLLat * kLNB>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            constexpr int e = j / (kLLat * kLNB), la = (j / kLNB) % kLLat, n = j % kLNB;
+            mfma16_tied<DT>(acc[la][n], a0[la], b0[n], e);
+            if constexpr (j < kLLat + kLNB) {
+                rd_op(a1, b1, 1, jc);
+            } else if constexpr (j < kLLat + kLNB + kLWChunks) {
+                constexpr int i = j - (kLLat + kLNB);
+                lds_load16(wr, wnx + (wave * 64 + 8 * i) * kStepBytes, tl ? tail_off(wvoff[i], i) : wvoff[i], so);
             }
-#pragma unroll
-            for (int fa = 0; fa < kLFrags; ++fa)
-#pragma unroll
-                for (int n = 0; n < kLNB; ++n) mfma_quad<DT>(acc[fa][n], wc[fa], cur[n]);
-            if (q == 0) issue_w(wnx);
-            if (q == 1) issue_x(xnx);
-            // (MFMA, DS read) x 8, then quads 0 and 1: (MFMA, LDS load) x 8; others: MFMA x 8
-            if (q < 3) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
-                }
-            }
-            if (q < 2) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM read (to LDS)
-                }
-            } else if (q < 3) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-            } else {
-                __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        });
+        // phase 1: (MFMA, X load) x 8, MFMA x the rest
+        static_for<E * kLLat * kLNB>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            constexpr int e = j / (kLLat * kLNB), la = (j / kLNB) % kLLat, n = j % kLNB;
+            mfma16_tied<DT>(acc[la][n], a1[la], b1[n], e);
+            if constexpr (j < kLXChunks)
+                lds_load16(xr, xnx + (wave * 64 + 8 * j) * kStepBytes, tl ? tail_off(xvoff[j], j) : xvoff[j], so);
+        });
+        ++ws;
+        ++xs;
     }
 };
 
@@ -258,7 +299,8 @@ size_t mainl_lds_bytes(int cap)
            (size_t)kLWaves * cap * 8 + (size_t)kLargeRows * sizeof(uint64_t*);
 }
 
-template <int DT, bool SAMPLE>
+// TAILK: built for a partial last d-step (d not a multiple of the step's elements)
+template <int DT, bool SAMPLE, bool TAILK>
 __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
 {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -281,9 +323,11 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
     // (a resource the compiler takes for divergent costs a waterfall loop
     // around every load).
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int h = lane >> 5, jl = lane & 31;
-    const int lw0 = (wave & 1) * (32 * kLFrags);   // this wave's first latent of the tile
-    const int rw0 = (wave >> 1) * (32 * kLNB);     // this wave's first row of the row block
+    // MFMA result layout: register r of block (la, n) of lane 16 g + i is
+    // latent lw0 + 16 la + 4 g + r of row rw0 + 16 n + i
+    const int i16 = lane & 15, g = lane >> 4;
+    const int lw0 = (wave & 1) * (16 * kLLat);   // this wave's first latent of the tile
+    const int rw0 = (wave >> 1) * (16 * kLNB);   // this wave's first row of the row block
 
     // workgroup -> (row block, W range): the row blocks of a W range share an XCD.
     // Sample mode: workgroup -> (row block, sample tile, d range).
@@ -323,7 +367,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
         }
     }
 
-    BigStream<DT, SAMPLE> bs;
+    BigStream<DT, SAMPLE, TAILK> bs;
     bs.W = (const unsigned char*)a.W;
     bs.row_bytes = a.d * Dt<DT>::esize;
     bs.X = (const unsigned char*)a.X;
@@ -350,19 +394,15 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
     bs.tid = tid;
     bs.lane = lane;
     bs.wave = wave;
-    bs.h = h;
-    bs.jl = jl;
 
     if (bs.ntiles > 0) {
         bs.init();
 
-        f32x16 acc[kLFrags][kLNB];
+        f32x4 acc[kLLat][kLNB];
 #pragma unroll
-        for (int fa = 0; fa < kLFrags; ++fa)
+        for (int la = 0; la < kLLat; ++la)
 #pragma unroll
-            for (int n = 0; n < kLNB; ++n)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[fa][n][r] = 0.f;
+            for (int n = 0; n < kLNB; ++n) acc[la][n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
         for (int t = 0; t < bs.ntiles; ++t) {
             const int64_t tile0 = (bs.tile_begin + t) * kLTile;
@@ -390,6 +430,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                 __builtin_amdgcn_s_barrier();
                 bs.step(acc, wst1, xs1, wst0, xs0);   // loads W/X(s+2) into stage 0
             }
+            mfma_drain();
             // the loads past the last step (zeros) land before the rings are reused
             __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0)
             __syncthreads();
@@ -398,18 +439,16 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                 float* P = a.P + (int64_t)ks * a.p_split;
 #pragma unroll
                 for (int n = 0; n < kLNB; ++n) {
-                    const int64_t row = b0 + rw0 + 32 * n + jl;
+                    const int64_t row = b0 + rw0 + 16 * n + i16;
                     if (row < B) {
 #pragma unroll
-                        for (int fa = 0; fa < kLFrags; ++fa)
+                        for (int la = 0; la < kLLat; ++la) {
+                            const int64_t f = tile0 + lw0 + 16 * la + 4 * g;
+                            f32x4 v;
 #pragma unroll
-                            for (int r4 = 0; r4 < 4; ++r4) {
-                                const int64_t i = tile0 + lw0 + fa * 32 + r4 * 8 + h * 4;
-                                f32x4 v;
-#pragma unroll
-                                for (int e = 0; e < 4; ++e) v[e] = acc[fa][n][r4 * 4 + e];
-                                *(f32x4*)(P + row * a.p_row + i) = flush_denorm4(v);
-                            }
+                            for (int e = 0; e < 4; ++e) v[e] = agpr_read(acc[la][n][e]);
+                            *(f32x4*)(P + row * a.p_row + f) = flush_denorm4(v);
+                        }
                     }
                 }
                 continue;
@@ -418,78 +457,84 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
             __syncthreads();
 
             // ---- epilogue: bias, threshold filter, append to the row segments ----
-            // One row block at a time, with no barrier between blocks.  Its 64
-            // scores per lane are read from the accumulators once, in
-            // straight-line code, biased and compared with the row threshold;
-            // they go to this wave's LDS staging area ([bit][lane], in the idle W
-            // ring), where the survivor walk reads them back.  Bit 16*fa + r of a
-            // row mask is latent lat0 + fa*32 + 8*(r/4) + r%4; this lane's row is
-            // rw0 + 32*n + jl.  Survivors that find their row segment full are
-            // kept in ovf[n] and handled after one barrier for the whole tile.
+            // Two row blocks (2 p, 2 p + 1) per round, with no barrier between
+            // rounds.  Their 64 scores per lane are read from the accumulators
+            // once, in straight-line code, biased and compared with the rows'
+            // thresholds; they go to this wave's LDS staging area ([bit][lane],
+            // in the idle W ring), where the survivor walk reads them back.  Bit
+            // 32 s + 4 la + r of a round's mask is latent lat0 + 16 la + r of
+            // row rw0 + 16 (2 p + s) + i16.  Survivors that find their row
+            // segment full are kept in ovf[p] and handled after one barrier for
+            // the whole tile.
             const bool edge = tile0 + kLTile > F ||
                               (a.sampled && (is_sampled(tile0, a.samp_log2, a.samp_blocks) ||
                                              is_sampled(tile0 + kLTile - 1, a.samp_log2, a.samp_blocks)));
-            const int lat0 = (int)tile0 + lw0 + h * 4;
-            const float* bias_l = bias_s + lw0 + h * 4;   // + fa*32 + 8*(r/4) + r%4
+            const int lat0 = (int)tile0 + lw0 + 4 * g;
             // latents past F or in the sample are never candidates here
             uint64_t vmask = ~0ull;
             if (edge) {
-                vmask = 0;
+                uint32_t vm = 0;
 #pragma unroll
-                for (int bit = 0; bit < 16 * kLFrags; ++bit) {
-                    const int64_t f = lat0 + (bit >> 4) * 32 + ((bit & 15) >> 2) * 8 + (bit & 3);
+                for (int bit = 0; bit < 32; ++bit) {
+                    const int64_t f = lat0 + 16 * (bit >> 2) + (bit & 3);
                     const bool ok = f < F && !(a.sampled && is_sampled(f, a.samp_log2, a.samp_blocks));
-                    vmask |= ok ? (1ull << bit) : 0ull;
+                    vm |= ok ? (1u << bit) : 0u;
                 }
+                vmask = ((uint64_t)vm << 32) | vm;
             }
             // This wave's staging area: [lane][64 scores]; 16-byte chunk c of a
             // lane's 256 bytes sits in slot c ^ (lane & 15), so that the b128
             // writes of 16 consecutive lanes hit distinct banks.
-            float* stage = (float*)wst0 + wave * (16 * kLFrags * 64);
+            float* stage = (float*)wst0 + wave * (64 * 64);
             // This wave's survivor descriptors (the X ring is idle): up to 64 per lane.
             uint32_t* dlist = (uint32_t*)xs0 + wave * (64 * 64);
             auto stage_at = [&](int ln, int bit) -> float {
                 return stage[ln * 64 + ((((bit >> 2) ^ (ln & 15))) << 2) + (bit & 3)];
             };
-            // Stages row block n's biased scores; returns the mask of those not
-            // below threshold tv.
-            // this lane's 64 bias values, in registers for all row blocks
-            f32x4 bias_r[kLFrags * 4];
+            // this lane's 32 bias values, in registers for all rounds
+            f32x4 bias_r[kLLat];
 #pragma unroll
-            for (int i = 0; i < kLFrags * 4; ++i) bias_r[i] = *(const f32x4*)(bias_l + (i >> 2) * 32 + 8 * (i & 3));
-            auto stage_block = [&](auto nc, float tv) -> uint64_t {
-                constexpr int n = decltype(nc)::value;
+            for (int la = 0; la < kLLat; ++la) bias_r[la] = *(const f32x4*)(bias_s + lw0 + 16 * la + 4 * g);
+            // Stages round p's biased scores; returns the mask of those not
+            // below their row's threshold (t0: row block 2 p, t1: 2 p + 1).
+            auto stage_pair = [&](auto pc, float t0, float t1) -> uint64_t {
+                constexpr int p = decltype(pc)::value;
                 uint64_t msk = 0;
 #pragma unroll
-                for (int fa = 0; fa < kLFrags; ++fa) {
+                for (int s2 = 0; s2 < 2; ++s2) {
+                    const float tv = s2 ? t1 : t0;
                     uint32_t m = 0;
 #pragma unroll
-                    for (int r4 = 3; r4 >= 0; --r4) {
-                        const f32x4 bv = bias_r[fa * 4 + r4];
+                    for (int la = kLLat - 1; la >= 0; --la) {
+                        const f32x4 bv = bias_r[la];
                         f32x4 v;
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) v[e] = agpr_read(acc[fa][n][4 * r4 + e]) + bv[e];
-                        *(f32x4*)(stage + lane * 64 + (((4 * fa + r4) ^ (lane & 15)) << 2)) = v;
+                        for (int e = 0; e < 4; ++e) v[e] = agpr_read(acc[la][2 * p + s2][e]) + bv[e];
+                        *(f32x4*)(stage + lane * 64 + (((8 * s2 + la) ^ (lane & 15)) << 2)) = v;
 #pragma unroll
-                        for (int e = 3; e >= 0; --e) m = mask_step(m, v[e], tv);   // bits 15 .. 0
+                        for (int e = 3; e >= 0; --e) m = mask_step(m, v[e], tv);   // bits 31 .. 0
                     }
-                    msk |= (uint64_t)m << (16 * fa);
+                    msk |= (uint64_t)m << (32 * s2);
                 }
                 return msk;
             };
-            // Appends the staged scores of the bits of pend (row block n) to the
+            // Appends the staged scores of the bits of pend (round p) to the
             // rows' segments; returns the bits that found their segment full.
             // The lanes' survivors are spread over the whole wave: each lane
             // lists its own as descriptors (slot, bit, lane) at its offset in the
             // wave's list, then every lane stores one listed survivor per round.
-            auto append = [&](auto nc, uint64_t pend) -> uint64_t {
-                constexpr int n = decltype(nc)::value;
-                const int row = rw0 + 32 * n + jl;
-                const int c = __popcll(pend);
-                const int base = c ? atomicAdd(&cnt[row], c) : 0;
+            auto append = [&](auto pc, uint64_t pend) -> uint64_t {
+                constexpr int p = decltype(pc)::value;
+                const int row0 = rw0 + 32 * p + i16;   // row of bits 0 .. 31; + 16 for 32 .. 63
+                const uint32_t lo = (uint32_t)pend, hi = (uint32_t)(pend >> 32);
+                const int c0 = __popc(lo), c1 = __popc(hi);
+                const int base0 = c0 ? atomicAdd(&cnt[row0], c0) : 0;
+                const int base1 = c1 ? atomicAdd(&cnt[row0 + 16], c1) : 0;
                 __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
-                int nfit = cap - base;
-                nfit = nfit < 0 ? 0 : (nfit > c ? c : nfit);
+                int nf0 = cap - base0, nf1 = cap - base1;
+                nf0 = nf0 < 0 ? 0 : (nf0 > c0 ? c0 : nf0);
+                nf1 = nf1 < 0 ? 0 : (nf1 > c1 ? c1 : nf1);
+                const int nfit = nf0 + nf1;
                 // exclusive prefix sum of nfit (<= 64) over the wave, from its bit planes
                 int off = 0, total = 0;
 #pragma unroll
@@ -499,22 +544,28 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u)) << bp;
                     total += __popcll(bal) << bp;
                 }
-                uint64_t mm = pend;
-                for (int i = 0; i < nfit; ++i) {
-                    const int bit = __builtin_ctzll(mm);
-                    mm &= mm - 1u;
-                    dlist[off + i] = ((uint32_t)(base + i) << 12) | ((uint32_t)bit << 6) | (uint32_t)lane;
+                uint32_t m0 = lo, m1 = hi;
+                for (int j = 0; j < nf0; ++j) {
+                    const int bit = __builtin_ctz(m0);
+                    m0 &= m0 - 1u;
+                    dlist[off + j] = ((uint32_t)(base0 + j) << 12) | ((uint32_t)bit << 6) | (uint32_t)lane;
+                }
+                for (int j = 0; j < nf1; ++j) {
+                    const int bit = __builtin_ctz(m1);
+                    m1 &= m1 - 1u;
+                    dlist[off + nf0 + j] =
+                        ((uint32_t)(base1 + j) << 12) | ((uint32_t)(32 + bit) << 6) | (uint32_t)lane;
                 }
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 for (int j = lane; j < total; j += 64) {
                     const uint32_t dsc = dlist[j];
                     const int ln = dsc & 63, bit = (dsc >> 6) & 63, slot = (int)(dsc >> 12);
-                    const int lat = (int)tile0 + lw0 + (ln >> 5) * 4 + (bit >> 4) * 32 + ((bit & 15) >> 2) * 8 + (bit & 3);
-                    qrow[rw0 + 32 * n + (ln & 31)][slot] = make_key(stage_at(ln, bit), lat);
+                    const int lat = (int)tile0 + lw0 + 4 * (ln >> 4) + 16 * ((bit >> 2) & 7) + (bit & 3);
+                    qrow[rw0 + 32 * p + 16 * (bit >> 5) + (ln & 15)][slot] = make_key(stage_at(ln, bit), lat);
                 }
                 __builtin_amdgcn_wave_barrier();
-                return mm;
+                return ((uint64_t)m1 << 32) | m0;
             };
             if (a.xch && t == 0) {
                 // ---- threshold exchange after the first tile (MainArgs::xch's,
@@ -528,26 +579,29 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                 uint64_t* xmax = a.xmax + rbl * kLargeRows * nw;   // [kLargeRows][nw]
                 uint64_t* xthr = a.xthr + rbl * kLargeRows;        // [kLargeRows]
                 // 1. per row of this wave, the largest score (NaN left out) of
-                //    each 64-latent half of its 128 latents
+                //    each 64-latent half of its 128 latents: latent blocks
+                //    4 q .. 4 q + 3, over the four lane groups
                 static_for<kLNB>([&](auto nc) {
                     constexpr int n = decltype(nc)::value;
-                    const int row = rw0 + 32 * n + jl;
+                    const int row = rw0 + 16 * n + i16;
 #pragma unroll
                     for (int q = 0; q < 2; ++q) {
                         float m = -__builtin_inff();
 #pragma unroll
-                        for (int f2 = 0; f2 < 2; ++f2) {
-                            const int fa = 2 * q + f2;
+                        for (int l4 = 0; l4 < 4; ++l4) {
+                            const int la = 4 * q + l4;
 #pragma unroll
-                            for (int r = 0; r < 16; ++r) {
-                                const float v = agpr_read(acc[fa][n][r]) + bias_r[fa * 4 + (r >> 2)][r & 3];
-                                m = __builtin_fmaxf(m, ((vmask >> (16 * fa + r)) & 1ull) ? v : -__builtin_inff());
+                            for (int r = 0; r < 4; ++r) {
+                                const float v = agpr_read(acc[la][n][r]) + bias_r[la][r];
+                                m = __builtin_fmaxf(m, ((vmask >> (4 * la + r)) & 1ull) ? v : -__builtin_inff());
                             }
                         }
                         uint32_t o = ordered_u32(m);
-                        const uint32_t o2 = __shfl_xor(o, 32);
+                        uint32_t o2 = __shfl_xor(o, 16);
                         o = o2 > o ? o2 : o;
-                        if (h == 0 && row < nrows)
+                        o2 = __shfl_xor(o, 32);
+                        o = o2 > o ? o2 : o;
+                        if (g == 0 && row < nrows)
                             xch_put(xmax + (int64_t)row * nw + rg * kLXchPerWg + (wave & 1) * 2 + q, tag, o);
                     }
                 });
@@ -580,26 +634,28 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                 }
                 __syncthreads();
             }
-            uint64_t ovf[kLNB];
-            static_for<kLNB>([&](auto nc) {
-                constexpr int n = decltype(nc)::value;
-                const int row = rw0 + 32 * n + jl;
-                const uint64_t tk = thr[row];
-                uint64_t pend = stage_block(nc, tk ? key_value(tk) : -__builtin_inff());
-                pend = (b0 + row < B) ? (pend & vmask) : 0ull;
-                ovf[n] = append(nc, pend);
+            uint64_t ovf[kLPairs];
+            static_for<kLPairs>([&](auto pc) {
+                constexpr int p = decltype(pc)::value;
+                const int row0 = rw0 + 32 * p + i16;
+                const uint64_t tk0 = thr[row0], tk1 = thr[row0 + 16];
+                uint64_t pend = stage_pair(pc, tk0 ? key_value(tk0) : -__builtin_inff(),
+                                           tk1 ? key_value(tk1) : -__builtin_inff());
+                const uint64_t rows_ok = (b0 + row0 < B ? 0xFFFFFFFFull : 0ull) |
+                                         (b0 + row0 + 16 < B ? 0xFFFFFFFF00000000ull : 0ull);
+                ovf[p] = append(pc, pend & vmask & rows_ok);
             });
             if (__syncthreads_or((ovf[0] | ovf[1] | ovf[2] | ovf[3]) != 0)) {
-                // Rare: some row segments are full.  Block by block: compact the
+                // Rare: some row segments are full.  Round by round: compact the
                 // full segments to their top k (which raises their thresholds),
                 // drop the pending scores now below threshold, append the rest;
                 // repeat until nothing is pending.
-                static_for<kLNB>([&](auto nc) {
-                    constexpr int n = decltype(nc)::value;
-                    const int row = rw0 + 32 * n + jl;
-                    uint64_t pend = ovf[n];
+                static_for<kLPairs>([&](auto pc) {
+                    constexpr int p = decltype(pc)::value;
+                    const int row0 = rw0 + 32 * p + i16;
+                    uint64_t pend = ovf[p];
                     if (!__syncthreads_or(pend != 0)) return;
-                    stage_block(nc, 0.f);   // this block's scores back into the staging area
+                    stage_pair(pc, 0.f, 0.f);   // this round's scores back into the staging area
                     for (int it = 0;; ++it) {
                         if (it >= a.max_rounds) {
                             // unreachable by the bound's argument (kMainLMaxRounds):
@@ -613,26 +669,25 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                                                                [&](int r) { return qrow[r]; }, cap, k, wave, lane);
                         __threadfence_block();
                         __syncthreads();
-                        // drop pending scores that fell below the raised threshold
-                        const uint64_t tk = thr[row];
+                        // drop pending scores that fell below the raised thresholds
+                        const uint64_t tk0 = thr[row0], tk1 = thr[row0 + 16];
                         uint64_t mm2 = pend;
                         while (mm2) {
                             const int bit = __builtin_ctzll(mm2);
                             mm2 &= mm2 - 1u;
-                            const int off = (bit >> 4) * 32 + ((bit & 15) >> 2) * 8 + (bit & 3);
-                            if (!(make_key(stage_at(lane, bit), lat0 + off) > tk)) pend &= ~(1ull << bit);
+                            const int off = 16 * ((bit >> 2) & 7) + (bit & 3);
+                            if (!(make_key(stage_at(lane, bit), lat0 + off) > ((bit >> 5) ? tk1 : tk0)))
+                                pend &= ~(1ull << bit);
                         }
-                        pend = append(nc, pend);
+                        pend = append(pc, pend);
                         if (!__syncthreads_or(pend != 0)) break;
                     }
                 });
             }
 #pragma unroll
-            for (int fa = 0; fa < kLFrags; ++fa)
+            for (int la = 0; la < kLLat; ++la)
 #pragma unroll
-                for (int n = 0; n < kLNB; ++n)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[fa][n][r] = 0.f;
+                for (int n = 0; n < kLNB; ++n) acc[la][n] = f32x4{0.f, 0.f, 0.f, 0.f};
             // The epilogue issued a data-dependent number of queue stores, which
             // the compiler cannot count; waiting for them here lets it keep
             // exact vmcnt waits in the next tile's d-step loop.
@@ -648,15 +703,22 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
     }
 }
 
-template <int DT, bool SAMPLE>
-static hipError_t launch_mainl_t(const MainLArgs& a, int grid, hipStream_t st)
+template <int DT, bool SAMPLE, bool TAILK>
+static hipError_t launch_mainl_k(const MainLArgs& a, int grid, hipStream_t st)
 {
     const size_t lds = mainl_lds_bytes(a.cap);
-    auto kern = mainl_kernel<DT, SAMPLE>;
+    auto kern = mainl_kernel<DT, SAMPLE, TAILK>;
     hipError_t e = ensure_lds((const void*)kern, lds);
     if (e != hipSuccess) return e;
     launch(kern, dim3((unsigned)grid), dim3(kLargeThreads), lds, st, a);
     return hipGetLastError();
+}
+
+template <int DT, bool SAMPLE>
+static hipError_t launch_mainl_t(const MainLArgs& a, int grid, hipStream_t st)
+{
+    if (a.d % Dt<DT>::DS != 0) return launch_mainl_k<DT, SAMPLE, true>(a, grid, st);
+    return launch_mainl_k<DT, SAMPLE, false>(a, grid, st);
 }
 
 hipError_t launch_mainl(int dt, const MainLArgs& a, int grid, hipStream_t st)

@@ -7,6 +7,17 @@ by lane around every load (v_readfirstlane, s_and_saveexec, a branch back),
 which splits the MFMA / load interleave and cost 7-10 % of the kernel.  The
 kernel must also make no flat memory accesses (they count on the LDS counter,
 so an LDS wait would also wait for them) and use no scratch memory.
+
+The kernel's MFMAs are inline asm, which the compiler's hazard checks do not
+see into, so the required wait states are checked here on its output:
+  - an MFMA result read by a VALU instruction (v_accvgpr_read/mov, or a store
+    of AGPR data) at least 20 wait states after the last MFMA before it (the
+    largest requirement on gfx950: passes + 4 for a 16-pass MFMA);
+  - a VGPR written by a VALU instruction and read by an MFMA as an operand, or
+    an AGPR written by v_accvgpr_write/mov and read as the accumulator, at
+    least 2 wait states later;
+  - the accumulators stay in place: no AGPR moves or copies inside the d-step
+    loop (the pattern the builtin MFMAs fall into at this register pressure).
 """
 import os
 import re
@@ -33,8 +44,8 @@ def asm(tmp_path_factory):
     return out.read_text()
 
 
-def _kernel(asm, dt, sample):
-    name = f"_ZN3stk12mainl_kernelILi{dt}ELb{1 if sample else 0}EEEvNS_9MainLArgsE"
+def _kernel(asm, dt, sample, tail=False):
+    name = f"_ZN3stk12mainl_kernelILi{dt}ELb{1 if sample else 0}ELb{1 if tail else 0}EEEvNS_9MainLArgsE"
     a = asm.index(name + ":")
     body = asm[a:asm.index(".Lfunc_end", a)]
     # the kernel's metadata map: its keys are sorted, so it runs from the
@@ -60,8 +71,9 @@ def _loop_blocks(body):
 
 @pytest.mark.parametrize("dt", [0, 1, 2])
 @pytest.mark.parametrize("sample", [False, True])
-def test_dstep_loop_has_no_waterfall(asm, dt, sample):
-    body, _ = _kernel(asm, dt, sample)
+@pytest.mark.parametrize("tail", [False, True])
+def test_dstep_loop_has_no_waterfall(asm, dt, sample, tail):
+    body, _ = _kernel(asm, dt, sample, tail)
     loop = _loop_blocks(body)
     assert loop, "no MFMA block found"
     for blk in loop:
@@ -72,8 +84,198 @@ def test_dstep_loop_has_no_waterfall(asm, dt, sample):
 
 @pytest.mark.parametrize("dt", [0, 1, 2])
 @pytest.mark.parametrize("sample", [False, True])
-def test_no_flat_access_no_scratch(asm, dt, sample):
-    body, meta = _kernel(asm, dt, sample)
+@pytest.mark.parametrize("tail", [False, True])
+def test_no_flat_access_no_scratch(asm, dt, sample, tail):
+    body, meta = _kernel(asm, dt, sample, tail)
     assert not re.search(r"\bflat_(load|store|atomic)", body)
     assert re.search(r"\.private_segment_fixed_size:\s+0\b", meta)
     assert re.search(r"\.vgpr_spill_count:\s+0\b", meta)
+
+
+def _cfg(body):
+    """The kernel's basic blocks: a list of (instructions, successor indices),
+    each instruction as (mnemonic, operand text); labels, directives and
+    comments dropped."""
+    blocks, labels = [[]], {}
+    for line in body.split("\n"):
+        t = line.split(";")[0].strip()
+        if not t or t.startswith("."):
+            if t.endswith(":") and t.startswith(".LBB"):
+                if blocks[-1]:
+                    blocks.append([])
+                labels[t[:-1]] = len(blocks) - 1
+            continue
+        if t.endswith(":"):
+            continue
+        parts = t.split(None, 1)
+        blocks[-1].append((parts[0], parts[1] if len(parts) > 1 else ""))
+    out = []
+    for i, ins in enumerate(blocks):
+        succ, fall = [], True
+        for op, args in ins:
+            if op == "s_branch":
+                succ.append(labels[args.strip()])
+                fall = False
+            elif op.startswith("s_cbranch"):
+                succ.append(labels[args.strip()])
+            elif op == "s_endpgm":
+                fall = False
+        if fall and i + 1 < len(blocks):
+            succ.append(i + 1)
+        out.append((ins, succ))
+    return out
+
+
+def _preds(cfg):
+    preds = [[] for _ in cfg]
+    for i, (_, succ) in enumerate(cfg):
+        for j in succ:
+            preds[j].append(i)
+    return preds
+
+
+def _regs(text, kind):
+    """Register numbers of kind 'v' or 'a' named in an operand text."""
+    regs = set()
+    for lo, hi in re.findall(r"\b%s\[(\d+):(\d+)\]" % kind, text):
+        regs.update(range(int(lo), int(hi) + 1))
+    for r in re.findall(r"\b%s(\d+)\b" % kind, text):
+        regs.add(int(r))
+    return regs
+
+
+def _wait_states(ins):
+    return int(ins[1], 0) + 1 if ins[0] == "s_nop" else 1
+
+
+def _walk_back(cfg, preds, b, i, limit, hit):
+    """Every instruction on the paths that end just before instruction i of
+    block b, nearest first, until limit wait states: calls hit(ins, ws) with
+    the wait states between that instruction and the end; hit returns True to
+    stop the path there."""
+    stack, seen = [(b, i, 0)], set()
+    while stack:
+        b, i, ws = stack.pop()
+        if (b, i, ws) in seen:
+            continue
+        seen.add((b, i, ws))
+        ins = cfg[b][0]
+        stopped = False
+        for j in range(i - 1, -1, -1):
+            if ws >= limit or hit(ins[j], ws):
+                stopped = True
+                break
+            ws += _wait_states(ins[j])
+        if not stopped and ws < limit:
+            for p in preds[b]:
+                stack.append((p, len(cfg[p][0]), ws))
+
+
+def _is_acc_read(op, args):
+    return (op.startswith(("v_accvgpr_read", "v_accvgpr_mov")) or
+            (op.startswith(("global_store", "buffer_store", "ds_write")) and bool(_regs(args, "a"))))
+
+
+@pytest.mark.parametrize("dt", [0, 1, 2])
+@pytest.mark.parametrize("sample", [False, True])
+@pytest.mark.parametrize("tail", [False, True])
+def test_mfma_result_reads_wait(asm, dt, sample, tail):
+    """On every path into a VALU read of an AGPR, at least 20 wait states
+    separate it from the last MFMA."""
+    body, _ = _kernel(asm, dt, sample, tail)
+    cfg = _cfg(body)
+    preds = _preds(cfg)
+    reads = 0
+    for b, (ins, _) in enumerate(cfg):
+        for i, (op, args) in enumerate(ins):
+            if not _is_acc_read(op, args):
+                continue
+            reads += 1
+
+            def hit(x, ws):
+                assert not x[0].startswith("v_mfma"), f"{op} {args}: {ws} wait states after {x[0]} {x[1]}"
+                return False
+            _walk_back(cfg, preds, b, i, 20, hit)
+    assert reads > 0
+
+
+@pytest.mark.parametrize("dt", [0, 1, 2])
+@pytest.mark.parametrize("sample", [False, True])
+@pytest.mark.parametrize("tail", [False, True])
+def test_mfma_operands_not_fresh_from_valu(asm, dt, sample, tail):
+    """On every path into an MFMA, no VALU instruction writes a VGPR it reads,
+    and no v_accvgpr_write/mov an AGPR it reads, within 2 wait states."""
+    body, _ = _kernel(asm, dt, sample, tail)
+    cfg = _cfg(body)
+    preds = _preds(cfg)
+    nmfma = 0
+    for b, (ins, _) in enumerate(cfg):
+        for i, (op, args) in enumerate(ins):
+            if not op.startswith("v_mfma"):
+                continue
+            nmfma += 1
+            srcs = args.partition(",")[2]
+            src_v, src_a = _regs(srcs, "v"), _regs(srcs, "a")
+
+            def hit(x, ws):
+                pop, pargs = x
+                pdst = pargs.split(",")[0]
+                if pop.startswith(("v_accvgpr_write", "v_accvgpr_mov")):
+                    assert not (_regs(pdst, "a") & src_a), f"{op} {args} reads {pdst} of {pop} after {ws}"
+                elif pop.startswith("v_") and not pop.startswith(("v_mfma", "v_readlane", "v_readfirstlane",
+                                                                  "v_cmp")):
+                    assert not (_regs(pdst, "v") & src_v), f"{op} {args} reads {pdst} of {pop} after {ws}"
+                return False
+            _walk_back(cfg, preds, b, i, 2, hit)
+    assert nmfma > 0
+
+
+@pytest.mark.parametrize("dt", [0, 1, 2])
+@pytest.mark.parametrize("sample", [False, True])
+@pytest.mark.parametrize("tail", [False, True])
+def test_accumulators_stay_in_place(asm, dt, sample, tail):
+    body, _ = _kernel(asm, dt, sample, tail)
+    for blk in _loop_blocks(body):
+        assert "v_accvgpr" not in blk
+        for m in re.finditer(r"v_mfma\S*\s+(a\[\d+:\d+\]),[^\n]*,\s*(a\[\d+:\d+\])", blk):
+            assert m.group(1) == m.group(2), m.group(0)
+
+
+def test_hazard_walk_sees_across_blocks():
+    """The checks' own test, on hand-written text: a read 3 wait states after
+    an MFMA in the block before, and an MFMA operand written by the VALU just
+    before it in the block before, are both found."""
+    body = "\n".join([
+        "k:",
+        "\tv_mfma_f32_16x16x32_bf16 a[0:3], v[0:3], v[4:7], a[0:3]",
+        "\ts_cbranch_scc0 .LBB0_2",
+        ".LBB0_1:",
+        "\ts_nop 1",
+        "\tv_accvgpr_read_b32 v8, a0",
+        ".LBB0_2:",
+        "\tv_mov_b32_e32 v5, 0",
+        "\ts_branch .LBB0_3",
+        ".LBB0_3:",
+        "\tv_mfma_f32_16x16x32_bf16 a[4:7], v[0:3], v[4:7], a[4:7]",
+        "\ts_endpgm",
+    ])
+    cfg = _cfg(body)
+    preds = _preds(cfg)
+    assert [s for _, s in cfg] == [[2, 1], [2], [3], []]
+    found = []
+
+    def hit(x, ws):
+        if x[0].startswith("v_mfma"):
+            found.append(("mfma", ws))
+            return True
+        return False
+    _walk_back(cfg, preds, 1, 1, 20, hit)
+    assert found == [("mfma", 3)]
+    found.clear()
+
+    def hit2(x, ws):
+        if x[0].startswith("v_mov"):
+            found.append(("valu", ws))
+        return False
+    _walk_back(cfg, preds, 3, 0, 2, hit2)
+    assert found == [("valu", 1)]
