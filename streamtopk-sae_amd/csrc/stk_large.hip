@@ -219,9 +219,10 @@ struct BigStream {
     // of the 16-byte operands per round of 64).  The operands of phase 0 are
     // read up front; phase 1's are read during phase 0's MFMAs, one read
     // between MFMAs.  The next d-step's LDS loads are folded into the MFMA
-    // stream too -- W(s+1) into wnx during phase 0, X(s+1) into xnx during
-    // phase 1, one load instruction between MFMAs -- so that the texture path
-    // works in the background instead of stalling the wave's in-order issue.
+    // stream too -- W(s+1) into wnx at the start of phase 0, X(s+1) into xnx
+    // at the start of phase 1, one load instruction between MFMAs -- so that
+    // the texture path works in the background instead of stalling the wave's
+    // in-order issue.
     // The MFMAs are volatile asm (mfma16_tied), so this program order is the
     // issue order.
     __device__ __forceinline__ void step(f32x4 (&acc)[kLLat][kLNB], const unsigned char* wst,
@@ -247,17 +248,17 @@ struct BigStream {
         };
         static_for<kLLat + kLNB>([&](auto rc) { rd_op(a0, b0, 0, rc); });
         constexpr int E = DT == DT_F32 ? 4 : 1;   // MFMA rounds per phase
-        // phase 0: (MFMA, DS read) x 16, (MFMA, W load) x 8, MFMA x the rest
+        // phase 0: (MFMA, DS read, W load) x 8, (MFMA, DS read) x 8, MFMA x the
+        // rest.  W comes from HBM: its loads go first, to land by the step's end
+        // (later W loads, or X loads in phase 0 with the DS reads, measured
+        // 1-9 % slower at B = 1024).
         static_for<E * kLLat * kLNB>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
             constexpr int e = j / (kLLat * kLNB), la = (j / kLNB) % kLLat, n = j % kLNB;
             mfma16_tied<DT>(acc[la][n], a0[la], b0[n], e);
-            if constexpr (j < kLLat + kLNB) {
-                rd_op(a1, b1, 1, jc);
-            } else if constexpr (j < kLLat + kLNB + kLWChunks) {
-                constexpr int i = j - (kLLat + kLNB);
-                lds_load16(wr, wnx + (wave * 64 + 8 * i) * kStepBytes, tl ? tail_off(wvoff[i], i) : wvoff[i], so);
-            }
+            if constexpr (j < kLLat + kLNB) rd_op(a1, b1, 1, jc);
+            if constexpr (j < kLWChunks)
+                lds_load16(wr, wnx + (wave * 64 + 8 * j) * kStepBytes, tl ? tail_off(wvoff[j], j) : wvoff[j], so);
         });
         // phase 1: (MFMA, X load) x 8, MFMA x the rest
         static_for<E * kLLat * kLNB>([&](auto jc) {
