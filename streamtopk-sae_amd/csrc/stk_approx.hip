@@ -378,6 +378,7 @@ __global__ __launch_bounds__(kThreads) void cand_kernel(CandArgs a)
     const int kk = k < c ? k : c;
     int64_t g0 = tid;
     int u0 = 0, e0 = 0;   // resume point after a full buffer
+    uint32_t vpar = 0;    // block_any's call parity
     for (;;) {
         const uint64_t thr = S.thr;
         bool stalled = false;
@@ -408,7 +409,7 @@ __global__ __launch_bounds__(kThreads) void cand_kernel(CandArgs a)
         }
         __syncthreads();
         if (S.cnt >= kSelCap) select_compact(S, kSelCap, k, tid);
-        if (!__syncthreads_or(stalled)) break;
+        if (!block_any<kThreads / 64>(stalled, S.vote, vpar, tid >> 6, tid & 63)) break;
     }
     const int n = S.cnt < kSelCap ? S.cnt : kSelCap;
     if (n > k) select_compact(S, n, k, tid);

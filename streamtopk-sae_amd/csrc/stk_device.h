@@ -201,6 +201,39 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, unsigned ch
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)ldsbase, 16, voff, soff, 0, 0);
 }
 
+// ---------------------------------------------------------------------------
+// Workgroup-wide OR of p.  Every thread of the workgroup calls it, the same
+// number of times.  HIP's __syncthreads_or reads the workgroup size from the
+// kernel's implicit arguments, and where registers are short the compiler
+// reloads it at every call (a scalar memory load and its wait).  Here lane 0
+// of each wave stores whether any lane of the wave has p into the wave's
+// slot, one barrier, and every lane reads all slots.  The slots alternate
+// between two sets from call to call (parity, a per-thread call counter), so a
+// wave's store for the next call cannot meet a slower wave's read of this one:
+// the next call's barrier lies between them.  vote: 2 * WAVES words of LDS,
+// 16-byte aligned.
+// ---------------------------------------------------------------------------
+template <int WAVES>
+__device__ __forceinline__ bool block_any(bool p, uint32_t* vote, uint32_t& parity, int wave, int lane)
+{
+    uint32_t* v = vote + (parity & 1u) * WAVES;
+    ++parity;
+    const bool wp = __ballot(p) != 0;
+    if (lane == 0) v[wave] = wp ? 1u : 0u;
+    __syncthreads();
+    if constexpr (WAVES % 4 == 0) {
+        u32x4 acc = *(const u32x4*)v;
+#pragma unroll
+        for (int w = 4; w < WAVES; w += 4) acc |= *(const u32x4*)(v + w);
+        return (acc[0] | acc[1] | acc[2] | acc[3]) != 0u;
+    } else {
+        uint32_t acc = 0;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) acc |= v[w];
+        return acc != 0u;
+    }
+}
+
 // Ring layout: row r's 16-byte chunk c sits in slot c ^ ((r >> 1) & 7) of the
 // row's 128 bytes, so that the MFMA-layout reads (32 rows x one chunk per
 // half-wave) hit 16 distinct 16-byte bank groups.

@@ -240,6 +240,8 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
     float* bias_lds = (float*)(gcnt + BT);                         // [2][kTileLatents]
     uint64_t* lqk = (uint64_t*)(bias_lds + 2 * kTileLatents);      // [BT][lq] LDS queues
     uint64_t* cscr = lqk + BT * lq;                                // [WAVES][cap] compaction scratch
+    uint32_t* vote = (uint32_t*)(cscr + WAVES * cap);              // [2][WAVES] block_any slots
+    uint32_t vpar = 0;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, jl = lane & 31;
@@ -351,7 +353,7 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
                 pend[n] = keep;
                 overflow |= keep != 0;
             }
-            if (!__syncthreads_or(overflow)) break;
+            if (!block_any<WAVES>(overflow, vote, vpar, wave, lane)) break;
             if (it >= a.max_rounds) {
                 // unreachable by the bound's argument (kMainMaxRounds): the
                 // pending scores are lost, so the call's result is marked
@@ -654,7 +656,8 @@ __global__ __launch_bounds__(NT) void thr_kernel(ThrArgs a)
 // the last compaction) go to S.buf; when it fills, it is compacted to its top
 // k, which raises `run`.  Every thread of the workgroup takes part.
 template <int N, int NT>
-__device__ __forceinline__ void merge_pass(SelSharedT<NT>& S, const uint64_t (&v)[N], int k, int tid, uint64_t& run)
+__device__ __forceinline__ void merge_pass(SelSharedT<NT>& S, const uint64_t (&v)[N], int k, int tid, uint64_t& run,
+                                           uint32_t& vpar)
 {
     static_assert(N <= 64, "pending mask");
     using Mask = std::conditional_t<(N > 32), uint64_t, uint32_t>;
@@ -683,7 +686,7 @@ __device__ __forceinline__ void merge_pass(SelSharedT<NT>& S, const uint64_t (&v
                 }
             }
         }
-        if (!__syncthreads_or(stalled)) break;
+        if (!block_any<NT / 64>(stalled, S.vote, vpar, tid >> 6, tid & 63)) break;
         select_compact(S, kSelCap, k, tid);   // S.cnt = k, S.thr = k-th key
         const uint64_t r2 = S.thr;
         run = r2;
@@ -782,6 +785,7 @@ __global__ __launch_bounds__(NT, kWaves) void merge_kernel(MergeArgs a)
         __syncthreads();
     }
     uint64_t run = 0;
+    uint32_t vpar = 0;   // block_any's call parity
     for (int64_t c0 = 0; c0 < n; c0 += (int64_t)kPer * NT) {
         if (nseg > 0) {
             // segment of each segment candidate: the number of segments whose
@@ -829,7 +833,7 @@ __global__ __launch_bounds__(NT, kWaves) void merge_kernel(MergeArgs a)
                     v[u] = ok ? keys[i] : 0ull;
             }
         }
-        merge_pass(S, v, k, tid, run);
+        merge_pass(S, v, k, tid, run, vpar);
     }
     auto out = [&](int r, uint64_t kk) {
         a.V[row * k + r] = key_value(kk);
@@ -879,6 +883,7 @@ __global__ __launch_bounds__(NT, kWaves) void merge_seg_kernel(MergeArgs a)
     }
     if (tid == 0) S.cnt = 0;
     uint64_t run = 0;
+    uint32_t vpar = 0;   // block_any's call parity
     for (int s0 = 0; s0 < nseg || s0 == 0; s0 += kSlots) {
         const int sg = s0 + slot;
         const bool own = sg < nseg;
@@ -909,9 +914,9 @@ __global__ __launch_bounds__(NT, kWaves) void merge_seg_kernel(MergeArgs a)
                 v[u] = o < cnt ? p[0] : 0ull;
                 v[u + 1] = o + 1 < cnt ? p[1] : 0ull;
             }
-            merge_pass(S, v, k, tid, run);
+            merge_pass(S, v, k, tid, run, vpar);
             if constexpr (kHead) v[kPer] = 0ull;
-            if (!__syncthreads_or(cnt > base + kStep - 2 * part)) break;
+            if (!block_any<NT / 64>(cnt > base + kStep - 2 * part, S.vote, vpar, tid >> 6, tid & 63)) break;
         }
     }
     emit_topk(S, k, tid, [&](int r, uint64_t kk) {
@@ -1021,12 +1026,12 @@ size_t main_lds_bytes(int NB, int cap, int lq)
 {
     const size_t BT = 32 * (size_t)NB;
     const size_t rings = 2 * (size_t)kTileLatents * kXRowStride + 2 * BT * kXRowStride;   // TileStream rings
-    return rings + BT * 8 + BT * 8 + 2 * kTileLatents * 4 + BT * (size_t)lq * 8 + (size_t)kMainWaves * cap * 8;
+    return rings + BT * 8 + BT * 8 + 2 * kTileLatents * 4 + BT * (size_t)lq * 8 + (size_t)kMainWaves * cap * 8 +
+           2 * kMainWaves * sizeof(uint32_t);
 }
 
 // LDS queue keys per row: the most (even, at most 64) whose LDS use, with
-// global segments of cap = k + lq keys, fits the workgroup's 160 KiB (less
-// 1 KiB for the kernel's static LDS: __syncthreads_or's reduction).
+// global segments of cap = k + lq keys, fits 159 KiB of the workgroup's 160.
 int main_lds_queue(int NB, int k)
 {
     for (int lq = 64; lq >= 2; lq -= 2) {

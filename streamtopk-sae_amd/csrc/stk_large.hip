@@ -297,7 +297,7 @@ __device__ __forceinline__ float agpr_read(float x)
 size_t mainl_lds_bytes(int cap)
 {
     return 2 * (size_t)kLWStage + 2 * (size_t)kLXStage + kLTile * sizeof(float) + kLargeRows * 8 + kLargeRows * 4 +
-           (size_t)kLWaves * cap * 8 + (size_t)kLargeRows * sizeof(uint64_t*);
+           (size_t)kLWaves * cap * 8 + (size_t)kLargeRows * sizeof(uint64_t*) + 2 * kLWaves * sizeof(uint32_t);
 }
 
 // TAILK: built for a partial last d-step (d not a multiple of the step's elements)
@@ -317,6 +317,8 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
     // the LDS waits (lgkmcnt) of the survivor walk would then wait for.
     gu64** qrow = (gu64**)(cnt + kLargeRows);
     uint64_t* cscr = (uint64_t*)(qrow + kLargeRows);                  // [waves][cap]
+    uint32_t* vote = (uint32_t*)(cscr + kLWaves * a.cap);            // [2][waves] block_any slots
+    uint32_t vpar = 0;
     const int cap = a.cap, k = a.k;
 
     // wave is read into a scalar register so that the compiler knows it is
@@ -646,7 +648,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                                          (b0 + row0 + 16 < B ? 0xFFFFFFFF00000000ull : 0ull);
                 ovf[p] = append(pc, pend & vmask & rows_ok);
             });
-            if (__syncthreads_or((ovf[0] | ovf[1] | ovf[2] | ovf[3]) != 0)) {
+            if (block_any<kLWaves>((ovf[0] | ovf[1] | ovf[2] | ovf[3]) != 0, vote, vpar, wave, lane)) {
                 // Rare: some row segments are full.  Round by round: compact the
                 // full segments to their top k (which raises their thresholds),
                 // drop the pending scores now below threshold, append the rest;
@@ -655,7 +657,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                     constexpr int p = decltype(pc)::value;
                     const int row0 = rw0 + 32 * p + i16;
                     uint64_t pend = ovf[p];
-                    if (!__syncthreads_or(pend != 0)) return;
+                    if (!block_any<kLWaves>(pend != 0, vote, vpar, wave, lane)) return;
                     stage_pair(pc, 0.f, 0.f);   // this round's scores back into the staging area
                     for (int it = 0;; ++it) {
                         if (it >= a.max_rounds) {
@@ -681,7 +683,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                                 pend &= ~(1ull << bit);
                         }
                         pend = append(pc, pend);
-                        if (!__syncthreads_or(pend != 0)) break;
+                        if (!block_any<kLWaves>(pend != 0, vote, vpar, wave, lane)) break;
                     }
                 });
             }

@@ -22,6 +22,7 @@ struct SelSharedT {
     };
     uint64_t wthr[NW];
     uint64_t prefix, mask, thr;
+    alignas(16) uint32_t vote[2 * NW];   // block_any slots
     uint32_t remaining;
     int cnt, sel_cnt, done;
 };
