@@ -316,6 +316,11 @@ LARGE = {
     "large_unsampled_ragged": dict(B=600, d=128, F=3000, k=16),
     "large_k64": dict(B=1024, d=512, F=40000, k=64),
     "large_sample8k": dict(B=520, d=128, F=70001, k=128),   # F >= 65536: 8192 sampled latents
+    # d not a multiple of the kernel's 64-element (fp32: 32) d-step: the
+    # instances built for a partial last step, with the exchange and with the
+    # sample pass
+    "large_tail_d200": dict(B=512, d=200, F=20000, k=64),
+    "large_tail_sampled_d72": dict(B=520, d=72, F=70001, k=128),
 }
 
 
