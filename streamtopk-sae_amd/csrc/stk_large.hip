@@ -79,17 +79,18 @@ __device__ __forceinline__ void static_for(Fn&& f)
 // FLOP/s than the 32x32 one under the power limit (1.99-2.01 against
 // 1.73-1.81 PF/s in an MFMA loop on random operands): the same products with
 // half the accumulator traffic per product.
-// Written as volatile asm with the accumulator tied to
-// its AGPRs: through the builtin, the compiler gives each of the 64 4-register
-// accumulators a new register per MFMA and copies them back around every
-// d-step (hundreds of AGPR/VGPR moves and spills per step), and volatile
-// keeps the MFMAs in program order with the reads and loads woven between
-// them.  The compiler's hazard checks do not look inside the asm: the
-// operands are only ever written by LDS reads (whose waits the compiler
-// counts), an MFMA's accumulator is next read by an MFMA 64 MFMAs later,
-// the zeros written into the accumulators at a tile's start are separated
-// from its first MFMA by the tile's first loads, barrier and operand reads
-// (2 wait states needed), and the reads of the results wait for mfma_drain.
+// Written as volatile asm with the accumulator tied to its AGPRs: through the
+// builtin, the compiler gives each of the 64 4-register accumulators a new
+// register per MFMA and copies them back around every d-step (hundreds of
+// AGPR/VGPR moves and spills per step), and volatile keeps the MFMAs in
+// program order with the reads and loads woven between them.  The compiler's
+// hazard checks do not look inside the asm: the operands are only ever
+// written by LDS reads (whose waits the compiler counts), an MFMA's
+// accumulator is next read by an MFMA 64 MFMAs later, the zeros written into
+// the accumulators at a tile's start are separated from its first MFMA by the
+// tile's first loads, barrier and operand reads (2 wait states needed), and
+// the reads of the results wait for mfma_drain (tests/test_isa.py checks each
+// of these on the compiled code).
 template <int DT>
 __device__ __forceinline__ void mfma16_tied(f32x4& acc, const u32x4& a, const u32x4& b, int e)
 {
