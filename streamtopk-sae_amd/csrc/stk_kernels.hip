@@ -240,7 +240,7 @@ __global__ __launch_bounds__(kMainThreads, 2) void main_kernel(MainArgs a)
     float* bias_lds = (float*)(gcnt + BT);                         // [2][kTileLatents]
     uint64_t* lqk = (uint64_t*)(bias_lds + 2 * kTileLatents);      // [BT][lq] LDS queues
     uint64_t* cscr = lqk + BT * lq;                                // [WAVES][cap] compaction scratch
-    uint32_t* vote = (uint32_t*)(cscr + WAVES * cap);              // [2][WAVES] block_any slots
+    uint32_t* vote = (uint32_t*)(cscr + WAVES * cap);              // [2][WAVES] block_any slots (cap even: 16-byte aligned)
     uint32_t vpar = 0;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;

@@ -318,7 +318,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
     // the LDS waits (lgkmcnt) of the survivor walk would then wait for.
     gu64** qrow = (gu64**)(cnt + kLargeRows);
     uint64_t* cscr = (uint64_t*)(qrow + kLargeRows);                  // [waves][cap]
-    uint32_t* vote = (uint32_t*)(cscr + kLWaves * a.cap);            // [2][waves] block_any slots
+    uint32_t* vote = (uint32_t*)(cscr + kLWaves * a.cap);            // [2][waves] block_any slots (cap even)
     uint32_t vpar = 0;
     const int cap = a.cap, k = a.k;
 
