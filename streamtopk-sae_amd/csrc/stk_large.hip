@@ -659,7 +659,7 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                     const int row0 = rw0 + 32 * p + i16;
                     uint64_t pend = ovf[p];
                     if (!block_any<kLWaves>(pend != 0, vote, vpar, wave, lane)) return;
-                    stage_pair(pc, 0.f, 0.f);   // this round's scores back into the staging area
+                    stage_pair(pc, 0.f, 0.f);   // this pair's scores back into the staging area
                     for (int it = 0;; ++it) {
                         if (it >= a.max_rounds) {
                             // unreachable by the bound's argument (kMainLMaxRounds):

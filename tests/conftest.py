@@ -4,6 +4,8 @@ import sys
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+# the directory the GPU runs bring back with their results
+TIE_LOG_DIR = os.path.join(ROOT, "gpurun_out")
 PKG_DIR = os.path.join(ROOT, "streamtopk-sae_amd")
 TESTS = os.path.dirname(os.path.abspath(__file__))
 for p in (PKG_DIR, ROOT, TESTS):
@@ -28,7 +30,7 @@ def pytest_terminal_summary(terminalreporter, exitstatus, config):
     """The parity checks' near-tie log (parity.TIE_LOG), kept short enough for
     the tail of a quiet run: one line per full-size configuration (its checks
     grouped), one per check with near-tie rows, and the totals; every check is
-    also written to gpurun_out/parity_ties.json."""
+    also written to parity_ties.json in the output directory (TIE_LOG_DIR)."""
     try:
         import parity
     except ImportError:
@@ -60,7 +62,7 @@ def pytest_terminal_summary(terminalreporter, exitstatus, config):
                   f"({ties / max(rows, 1):.3%}); {len(bounded)} checks held to the fp32 sum bound, "
                   f"largest err/bound {max((e['value_err_over_bound'] for e in bounded), default=0.0):.2g}")
     try:
-        out = os.path.join(ROOT, "gpurun_out")
+        out = TIE_LOG_DIR
         os.makedirs(out, exist_ok=True)
         with open(os.path.join(out, "parity_ties.json"), "w") as f:
             json.dump({"checks": log, "rows": rows, "tie_rows": ties}, f, indent=1)

@@ -17,9 +17,9 @@ max(|score|, 1)).
 Indices.  Index sets must be identical except where the differing latents'
 scores lie within the contract tolerance (rtol) of the row's k-th score:
 near-ties.  Every check records its row count and its near-tie rows in
-TIE_LOG, which the test session prints at its end (conftest.py) and writes to
-gpurun_out/parity_ties.json; a check may also bound the fraction of rows with
-near-ties (max_tie_frac).
+TIE_LOG, which the test session prints at its end and writes as JSON
+(conftest.py); a check may also bound the fraction of rows with near-ties
+(max_tie_frac).
 """
 import math
 
