@@ -52,6 +52,8 @@ constexpr int kLNB = 8;                      // 16-row blocks per wave
 constexpr int kLLat = 8;                     // 16-latent blocks per wave
 constexpr int kLPairs = kLNB / 2;            // epilogue rounds: two row blocks each
 constexpr int kLTile = 256;                  // latents per tile
+constexpr int kLDefer = 16;                  // MFMAs of each d-step issued after the next step's barrier
+static_assert(kLDefer <= 2 * 8 + 8, "one deferred MFMA per phase-0 operand read");
 static_assert(2 * 16 * kLLat == kLTile && 2 * 16 * kLNB == kLargeRows, "2 x 2 wave grid");
 constexpr int kLWChunks = kLTile * 8 / kLargeThreads;       // 16-byte W chunks per thread per d-step
 constexpr int kLWStage = kLTile * kStepBytes;               // W ring stage: 256 rows x 128 B (swizzled)
@@ -113,6 +115,7 @@ __device__ __forceinline__ void mfma_drain()
 
 template <int DT, bool SAMPLE, bool TAILK>
 struct BigStream {
+    static constexpr int E = DT == DT_F32 ? 4 : 1;   // MFMA rounds per phase
     const unsigned char* W;
     int64_t row_bytes;           // bytes of a W row and of an X row (d elements)
     const unsigned char* X;
@@ -127,8 +130,15 @@ struct BigStream {
     // load cursors (absolute d-steps), uniform
     int ws, xs;
     __amdgpu_buffer_rsrc_t wres, xres, zres;      // wres: this wave's 64-row run of the tile
-    int wvoff[kLWChunks];        // W LDS load i of this wave: this lane's source offset in the wave's run
-    int xvoff[kLXChunks];        // X LDS load i of this wave: this lane's source offset in the row block
+    // LDS load i of a wave reads rows 8 i + lane / 8 of the wave's 64-row run
+    // (W: of the tile; X: of the row block), chunk lane % 8 ^ xswz(row).
+    // xswz(row) depends on row % 16 only, so loads i and i + 2 share their
+    // chunk and lie 16 rows apart: load i's source offset is vb[i % 2] +
+    // (i / 2) * rows16 (X: + xrun).
+    int vb[2];                   // this lane's source offsets of loads 0 and 1
+    int vbt[2];                  // the same in the partial last d-step: beyond every resource past d
+    int rows16;                  // bytes of 16 rows
+    int xrun;                    // bytes of the wave's 64-row X run into the row block
     int rd[2];                   // operand read offset of MFMA step m (row lane % 16 of block 0)
 
     __device__ __forceinline__ void init()
@@ -137,11 +147,14 @@ struct BigStream {
         // wave's 64-row run of the tile; X: of the row block): lane -> row +
         // lane / 8, slot lane % 8, which holds chunk slot ^ xswz(row)
 #pragma unroll
-        for (int i = 0; i < kLWChunks; ++i) {
-            const int r = 8 * i + (lane >> 3);   // row within the wave's 64
-            wvoff[i] = r * (int)row_bytes + (((lane & 7) ^ xswz(r)) * 16);
-            xvoff[i] = (wave * 64 + r) * (int)row_bytes + (((lane & 7) ^ xswz(r)) * 16);
+        for (int p = 0; p < 2; ++p) {
+            const int r = 8 * p + (lane >> 3);   // row within the wave's 64
+            const int chunk = (lane & 7) ^ xswz(r);
+            vb[p] = r * (int)row_bytes + chunk * 16;
+            vbt[p] = chunk * (16 / Dt<DT>::esize) < tail ? vb[p] : 0x40000000;
         }
+        rows16 = 16 * (int)row_bytes;
+        xrun = wave * 64 * (int)row_bytes;
         // lanes 16 g .. 16 g + 15 of MFMA step m read chunk 4 m + g of rows
         // 0 .. 15 of a block (rows 16 j + i share swizzle xswz(i))
         const int i = lane & 15, g = lane >> 4;
@@ -168,15 +181,11 @@ struct BigStream {
         }
     }
 
-    // The partial last d-step (tail != 0): a lane whose source chunk of load i
+    // Source offset of LDS load i from the pair of offsets b (vb, or vbt in
+    // the partial last d-step (tail != 0), where a lane whose source chunk
     // lies past d takes an offset beyond every resource's size, so the load
-    // returns zeros.
-    __device__ __forceinline__ int tail_off(int off, int i) const
-    {
-        const int r = 8 * i + (lane >> 3);
-        const int chunk = (lane & 7) ^ xswz(r);
-        return chunk * (16 / Dt<DT>::esize) < tail ? off : 0x40000000;
-    }
+    // returns zeros).
+    __device__ __forceinline__ int load_off(const int (&b)[2], int i) const { return b[i & 1] + (i >> 1) * rows16; }
 
     // W of step ws (zeros past s_hi) straight into the W stage, whole 128-byte
     // lines: this wave's 64-row run.
@@ -186,14 +195,10 @@ struct BigStream {
         const bool live = w < s_hi;
         const __amdgpu_buffer_rsrc_t r = live ? wres : zres;
         const int so = live ? w * kStepBytes : 0;
-        if (tail != 0 && w == nds - 1) {
+        const bool tl = tail != 0 && w == nds - 1;
+        const int b[2] = {tl ? vbt[0] : vb[0], tl ? vbt[1] : vb[1]};
 #pragma unroll
-            for (int i = 0; i < kLWChunks; ++i)
-                lds_load16(r, wst + (wave * 64 + 8 * i) * kStepBytes, tail_off(wvoff[i], i), so);
-        } else {
-#pragma unroll
-            for (int i = 0; i < kLWChunks; ++i) lds_load16(r, wst + (wave * 64 + 8 * i) * kStepBytes, wvoff[i], so);
-        }
+        for (int i = 0; i < kLWChunks; ++i) lds_load16(r, wst + (wave * 64 + 8 * i) * kStepBytes, load_off(b, i), so);
         ++ws;
     }
 
@@ -204,30 +209,35 @@ struct BigStream {
         const bool live = x < s_hi;
         const __amdgpu_buffer_rsrc_t r = live ? xres : zres;
         const int so = live ? x * kStepBytes : 0;
-        if (tail != 0 && x == nds - 1) {
+        const bool tl = tail != 0 && x == nds - 1;
+        const int b[2] = {tl ? vbt[0] : vb[0], tl ? vbt[1] : vb[1]};
 #pragma unroll
-            for (int i = 0; i < kLXChunks; ++i)
-                lds_load16(r, xst + (wave * 64 + 8 * i) * kStepBytes, tail_off(xvoff[i], i), so);
-        } else {
-#pragma unroll
-            for (int i = 0; i < kLXChunks; ++i) lds_load16(r, xst + (wave * 64 + 8 * i) * kStepBytes, xvoff[i], so);
-        }
+        for (int i = 0; i < kLXChunks; ++i)
+            lds_load16(r, xst + (wave * 64 + 8 * i) * kStepBytes, load_off(b, i) + xrun, so);
         ++xs;
     }
 
     // One d-step from LDS stages wst / xst: two MFMA phases m of k = 32 (half
     // the step's d each), 64 MFMAs apiece (fp32: 4 x 64 of k = 4, one element
     // of the 16-byte operands per round of 64).  The operands of phase 0 are
-    // read up front; phase 1's are read during phase 0's MFMAs, one read
-    // between MFMAs.  The next d-step's LDS loads are folded into the MFMA
-    // stream too -- W(s+1) into wnx at the start of phase 0, X(s+1) into xnx
-    // at the start of phase 1, one load instruction between MFMAs -- so that
-    // the texture path works in the background instead of stalling the wave's
+    // read at the step's start, after the barrier; the previous
+    // step's last kLDefer MFMAs (whose operands a1 / b1 still hold) go between
+    // those reads, so that the MFMAs are busy while the reads land (deferring
+    // 16 took c4's kernel from ~1735 to ~1700 us on one box; 8 did as well,
+    // 24 and 32 were slower).  Phase 1's operands are read during phase 0's
+    // MFMAs, one read between MFMAs, and its last kLDefer MFMAs are left to
+    // the next step (or to finish()).  Every accumulator still receives its
+    // products in d order, so the sums are those of the undeferred order.
+    // The next d-step's LDS loads are folded into the stream too -- W(s+1)
+    // into wnx with the first reads after the barrier, X(s+1) into xnx at the
+    // start of phase 1, one load instruction between MFMAs -- so that the
+    // texture path works in the background instead of stalling the wave's
     // in-order issue.
     // The MFMAs are volatile asm (mfma16_tied), so this program order is the
     // issue order.
-    __device__ __forceinline__ void step(f32x4 (&acc)[kLLat][kLNB], const unsigned char* wst,
-                                         const unsigned char* xst, unsigned char* wnx, unsigned char* xnx)
+    __device__ __forceinline__ void step(f32x4 (&acc)[kLLat][kLNB], u32x4 (&a1)[kLLat], u32x4 (&b1)[kLNB],
+                                         const unsigned char* wst, const unsigned char* xst, unsigned char* wnx,
+                                         unsigned char* xnx)
     {
         const unsigned char* wl = wst + (wave & 1) * (16 * kLLat) * kStepBytes;
         const unsigned char* xl = xst + (wave >> 1) * (16 * kLNB) * kStepBytes;
@@ -238,7 +248,11 @@ struct BigStream {
         // the next d-step is the partial last one (only kernels built for a
         // partial last step look)
         const bool tl = TAILK && w == nds - 1;
-        u32x4 a0[kLLat], b0[kLNB], a1[kLLat], b1[kLNB];
+        // the loads' offsets are formed in the step from two registers: opaque
+        // here, so that the compiler does not keep all 16 alive across the loop
+        int ob[2] = {tl ? vbt[0] : vb[0], tl ? vbt[1] : vb[1]};
+        asm volatile("" : "+v"(ob[0]), "+v"(ob[1]));
+        u32x4 a0[kLLat], b0[kLNB];
         // operand read r of a phase, in first-use order: W block 0, the X
         // blocks, W blocks 1 .. 7
         auto rd_op = [&](u32x4 (&av)[kLLat], u32x4 (&bv)[kLNB], int m, auto rc) {
@@ -247,30 +261,52 @@ struct BigStream {
             else if constexpr (r <= kLNB) bv[r - 1] = *(const u32x4*)(xl + rd[m] + (16 * (r - 1)) * kStepBytes);
             else av[r - kLNB] = *(const u32x4*)(wl + rd[m] + (16 * (r - kLNB)) * kStepBytes);
         };
-        static_for<kLLat + kLNB>([&](auto rc) { rd_op(a0, b0, 0, rc); });
-        constexpr int E = DT == DT_F32 ? 4 : 1;   // MFMA rounds per phase
-        // phase 0: (MFMA, DS read, W load) x 8, (MFMA, DS read) x 8, MFMA x the
-        // rest.  W comes from HBM: its loads go first, to land by the step's end
-        // (later W loads, or X loads in phase 0 with the DS reads, measured
-        // 1-9 % slower at B = 1024).
+        // after the barrier: (DS read, deferred MFMA, W load) x 8, (DS read,
+        // deferred MFMA) x 8.  W comes from HBM: its loads go first, to land by
+        // the step's end (W loads later in the step, or X loads in phase 0,
+        // measured 1-10 % slower at B = 1024).
+        static_for<kLLat + kLNB>([&](auto rc) {
+            rd_op(a0, b0, 0, rc);
+            if constexpr (decltype(rc)::value < kLDefer) deferred(acc, a1, b1, rc);
+            if constexpr (decltype(rc)::value < kLWChunks) {
+                constexpr int q = decltype(rc)::value;
+                lds_load16(wr, wnx + (wave * 64 + 8 * q) * kStepBytes, load_off(ob, q), so);
+            }
+        });
+        // phase 0: (MFMA, DS read) x 16, MFMA x the rest
         static_for<E * kLLat * kLNB>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
             constexpr int e = j / (kLLat * kLNB), la = (j / kLNB) % kLLat, n = j % kLNB;
             mfma16_tied<DT>(acc[la][n], a0[la], b0[n], e);
             if constexpr (j < kLLat + kLNB) rd_op(a1, b1, 1, jc);
-            if constexpr (j < kLWChunks)
-                lds_load16(wr, wnx + (wave * 64 + 8 * j) * kStepBytes, tl ? tail_off(wvoff[j], j) : wvoff[j], so);
         });
-        // phase 1: (MFMA, X load) x 8, MFMA x the rest
-        static_for<E * kLLat * kLNB>([&](auto jc) {
+        // phase 1: (MFMA, X load) x 8, MFMA x the rest but the last kLDefer
+        static_for<E * kLLat * kLNB - kLDefer>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
             constexpr int e = j / (kLLat * kLNB), la = (j / kLNB) % kLLat, n = j % kLNB;
             mfma16_tied<DT>(acc[la][n], a1[la], b1[n], e);
             if constexpr (j < kLXChunks)
-                lds_load16(xr, xnx + (wave * 64 + 8 * j) * kStepBytes, tl ? tail_off(xvoff[j], j) : xvoff[j], so);
+                lds_load16(xr, xnx + (wave * 64 + 8 * j) * kStepBytes, load_off(ob, j) + xrun, so);
         });
         ++ws;
         ++xs;
+    }
+
+    // Deferred MFMA r of a step: its phase-1 MFMA E * 64 - kLDefer + r.
+    template <class RC>
+    __device__ __forceinline__ static void deferred(f32x4 (&acc)[kLLat][kLNB], const u32x4 (&a1)[kLLat],
+                                                    const u32x4 (&b1)[kLNB], RC)
+    {
+        constexpr int j = E * kLLat * kLNB - kLDefer + RC::value;
+        constexpr int e = j / (kLLat * kLNB), la = (j / kLNB) % kLLat, n = j % kLNB;
+        mfma16_tied<DT>(acc[la][n], a1[la], b1[n], e);
+    }
+
+    // The last step's deferred MFMAs.
+    __device__ __forceinline__ static void finish(f32x4 (&acc)[kLLat][kLNB], const u32x4 (&a1)[kLLat],
+                                                  const u32x4 (&b1)[kLNB])
+    {
+        static_for<kLDefer>([&](auto rc) { deferred(acc, a1, b1, rc); });
     }
 };
 
@@ -425,15 +461,42 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
             bs.begin_tile(t);
             bs.issue_w(wst0);   // W(0)
             bs.issue_x(xs0);    // X(0)
-            // a padded last step (s >= nds) reads zeros: every step computes unconditionally
-            for (int s = 0; s < bs.nds2; s += 2) {
+            // a padded last step (s >= nds) reads zeros: every step computes
+            // unconditionally.  Every step takes the previous one's deferred
+            // MFMAs: the first step's operands a1 / b1 are zeros, which add
+            // exact zeros to the zero accumulators (a first step without them
+            // left the compiler free to place the accumulators' zeroing, and it
+            // moved live accumulators between registers).  The last step's
+            // deferred MFMAs run in finish().  The zeros pass through an empty
+            // asm, so that they are written here, before the first barrier
+            // (a VALU write of an MFMA operand needs 2 wait states before the
+            // MFMA), and so that the compiler does not take them from the
+            // zeroed accumulators.
+            u32x4 a1[kLLat], b1[kLNB];   // phase-1 operands, live into the next step
+#pragma unroll
+            for (int la = 0; la < kLLat; ++la) {
+                a1[la] = u32x4{0u, 0u, 0u, 0u};
+                asm volatile("" : "+v"(a1[la]));
+            }
+#pragma unroll
+            for (int n = 0; n < kLNB; ++n) {
+                b1[n] = u32x4{0u, 0u, 0u, 0u};
+                asm volatile("" : "+v"(b1[n]));
+            }
+            // nds2 >= 2 (d >= 1): a loop that cannot run zero times, so that no
+            // path around it joins the accumulators at finish() (the join made
+            // the compiler move accumulators between registers)
+            int s = 0;
+            do {
                 __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0): W/X(s) in stage 0
                 __builtin_amdgcn_s_barrier();         // ... for every wave; stage 1 free
-                bs.step(acc, wst0, xs0, wst1, xs1);   // loads W/X(s+1) into stage 1
+                bs.step(acc, a1, b1, wst0, xs0, wst1, xs1);   // loads W/X(s+1) into stage 1
                 __builtin_amdgcn_s_waitcnt(0x0070);
                 __builtin_amdgcn_s_barrier();
-                bs.step(acc, wst1, xs1, wst0, xs0);   // loads W/X(s+2) into stage 0
-            }
+                bs.step(acc, a1, b1, wst1, xs1, wst0, xs0);   // loads W/X(s+2) into stage 0
+                s += 2;
+            } while (s < bs.nds2);
+            bs.finish(acc, a1, b1);
             mfma_drain();
             // the loads past the last step (zeros) land before the rings are reused
             __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0)
