@@ -14,6 +14,10 @@
 //   - The next step's LDS loads are spread through the MFMAs (one per MFMA),
 //     not issued as a burst: with one wave per SIMD, a vector-memory
 //     instruction that cannot issue stalls the MFMAs behind it.
+//   - Each d-step's last 16 MFMAs are issued after the next step's barrier,
+//     between the reads of its first operands, so that the MFMAs do not sit
+//     idle while those reads land (the sums are unchanged: every
+//     accumulator still takes its products in d order).
 //   - The pipeline restarts at every tile, so the epilogue holds no prefetch.
 //   - bias: the tile's 256 values are loaded at the tile start and staged in
 //     LDS for the epilogue.
@@ -53,7 +57,7 @@ constexpr int kLLat = 8;                     // 16-latent blocks per wave
 constexpr int kLPairs = kLNB / 2;            // epilogue rounds: two row blocks each
 constexpr int kLTile = 256;                  // latents per tile
 constexpr int kLDefer = 16;                  // MFMAs of each d-step issued after the next step's barrier
-static_assert(kLDefer <= 2 * 8 + 8, "one deferred MFMA per phase-0 operand read");
+static_assert(kLDefer <= kLLat + kLNB, "one deferred MFMA per phase-0 operand read");
 static_assert(2 * 16 * kLLat == kLTile && 2 * 16 * kLNB == kLargeRows, "2 x 2 wave grid");
 constexpr int kLWChunks = kLTile * 8 / kLargeThreads;       // 16-byte W chunks per thread per d-step
 constexpr int kLWStage = kLTile * kStepBytes;               // W ring stage: 256 rows x 128 B (swizzled)
