@@ -321,6 +321,12 @@ LARGE = {
     # sample pass
     "large_tail_d200": dict(B=512, d=200, F=20000, k=64),
     "large_tail_sampled_d72": dict(B=520, d=72, F=70001, k=128),
+    # the d-step loop runs steps in pairs, each step also finishing the
+    # previous one's last MFMAs: an odd step count (a padded step of zeros),
+    # a single step (fp16/bf16), and a single partial step
+    "large_odd_steps_d192": dict(B=520, d=192, F=20000, k=64),
+    "large_one_step_d64": dict(B=512, d=64, F=5000, k=32),
+    "large_one_partial_step_d40": dict(B=512, d=40, F=3000, k=16),
 }
 
 
