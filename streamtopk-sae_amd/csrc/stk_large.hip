@@ -91,7 +91,8 @@ __device__ __forceinline__ void static_for(Fn&& f)
 // AGPR/VGPR moves and spills per step), and volatile keeps the MFMAs in
 // program order with the reads and loads woven between them.  The compiler's
 // hazard checks do not look inside the asm: the operands are only ever
-// written by LDS reads (whose waits the compiler counts), an MFMA's
+// written by LDS reads (whose waits the compiler counts) or zeroed before a
+// tile's first loads and barrier (2 wait states needed), an MFMA's
 // accumulator is next read by an MFMA 64 MFMAs later, the zeros written into
 // the accumulators at a tile's start are separated from its first MFMA by the
 // tile's first loads, barrier and operand reads (2 wait states needed), and
@@ -487,9 +488,10 @@ __global__ __launch_bounds__(kLargeThreads, 1) void mainl_kernel(MainLArgs a)
                 b1[n] = u32x4{0u, 0u, 0u, 0u};
                 asm volatile("" : "+v"(b1[n]));
             }
-            // nds2 >= 2 (d >= 1): a loop that cannot run zero times, so that no
-            // path around it joins the accumulators at finish() (the join made
-            // the compiler move accumulators between registers)
+            // nds2 >= 2 (d >= 1, and a sample-mode d range holds at least one
+            // step: ksplit <= nds): a loop that cannot run zero times, so that
+            // no path around it joins the accumulators at finish() (the join
+            // made the compiler move accumulators between registers)
             int s = 0;
             do {
                 __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0): W/X(s) in stage 0
