@@ -21,11 +21,18 @@
 namespace stk {
 
 constexpr int kOrdStride = kGroupTile + 4;   // LDS words per staged row (pad: no bank conflicts)
+// Group heads are collected in LDS over kHeadTiles tiles, so that each row's
+// heads reach global memory as whole 128-byte lines (16 groups of 8 bytes):
+// written tile by tile, 16 bytes of a line at a time, they cost c3's
+// group_kernel ~3-4 %.
+constexpr int kHeadTiles = 8;
+constexpr int kHeadSlots = 2 * kHeadTiles;   // groups per row and window
 
 size_t group_lds_bytes(int NB)
 {
     const size_t rings = 2 * (size_t)kGroupTile * kXRowStride + 2 * 32 * (size_t)NB * kXRowStride;
-    return rings + 2 * kGroupTile * sizeof(float) + 32 * (size_t)kOrdStride * sizeof(uint32_t);
+    return rings + 2 * kGroupTile * sizeof(float) + 32 * (size_t)kOrdStride * sizeof(uint32_t) +
+           32 * (size_t)NB * kHeadSlots * sizeof(uint64_t);
 }
 
 // Key of lane l ^ X within the lane's 16-lane row, X = 1 .. 15.  XOR 1, 3
@@ -152,10 +159,11 @@ __device__ __forceinline__ void bitonic_topc(T (&v)[8], int l)
 // (latents 128 g .. of tile `tile`), sorts them in registers (8 per lane)
 // and writes the group's top-c, descending, padded with (-FLT_MAX, -1) past
 // the end of F, for output row rowblk + rl (streamtopk_approx.cu:118-166).
-// Every lane of the wave takes part.
+// The group's head key goes to slot 2 (tile % kHeadTiles) + g of the row's
+// LDS head line hrow[rl].  Every lane of the wave takes part.
 template <int C>
-__device__ __forceinline__ void sort_segment(const GroupArgs& a, const uint32_t* ordv, int rl, int g, int l,
-                                             int64_t rowblk, int64_t tile)
+__device__ __forceinline__ void sort_segment(const GroupArgs& a, const uint32_t* ordv, uint64_t* hrow, int rl, int g,
+                                             int l, int64_t rowblk, int64_t tile)
 {
     constexpr int c = C;
     const int64_t B = a.B, G = a.num_groups;
@@ -264,7 +272,8 @@ __device__ __forceinline__ void sort_segment(const GroupArgs& a, const uint32_t*
         *(u32x4*)(a.cand_idxs + o + 4) = u32x4{idx[4], idx[5], idx[6], idx[7]};
         // the group's head (entry 0, this lane's first) as cand_kernel keys it
         if (l == 0)
-            a.heads[(rowblk + rlv) * G + grp] = idx[0] != 0xFFFFFFFFu ? make_key(val[0], (int32_t)idx[0]) : 0ull;
+            hrow[rl * kHeadSlots + 2 * (int)(tile % kHeadTiles) + g] =
+                idx[0] != 0xFFFFFFFFu ? make_key(val[0], (int32_t)idx[0]) : 0ull;
     }
 }
 
@@ -276,6 +285,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void group_kernel(GroupArgs a)
     extern __shared__ __align__(16) unsigned char smem[];
     float* bias_lds = (float*)(smem + TS::kRingBytes);             // [2][kGroupTile]
     uint32_t* ordv = (uint32_t*)(bias_lds + 2 * kGroupTile);       // [32 rows][kOrdStride]
+    uint64_t* hbuf = (uint64_t*)(ordv + 32 * kOrdStride);          // [32*NB rows][kHeadSlots] head keys
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, jl = lane & 31;
@@ -331,7 +341,22 @@ __global__ __launch_bounds__(kMainThreads, 1) void group_kernel(GroupArgs a)
             for (int rd = 0; rd < 2; ++rd) {
                 const int seg = wave * 8 + rd * 4 + sq;
                 const int rl = seg >> 1, g = seg & 1;
-                sort_segment<C>(a, ordv, rl, g, l, b0 + 32 * n, tile);
+                sort_segment<C>(a, ordv, hbuf + 32 * n * kHeadSlots, rl, g, l, b0 + 32 * n, tile);
+            }
+        }
+        // At the end of a head window (kHeadTiles aligned tiles) and after the
+        // workgroup's last tile: the window's heads, whole lines per row where
+        // the window is this workgroup's alone.  The next writes to hbuf come
+        // after the next tile's first d-step barrier.
+        if (tile % kHeadTiles == kHeadTiles - 1 || t == ts.ntiles - 1) {
+            __syncthreads();   // every segment's head is in hbuf
+            const int64_t wt = tile - tile % kHeadTiles;                    // the window's first tile
+            const int64_t g0 = 2 * (wt > ts.tile_begin ? wt : ts.tile_begin);
+            const int64_t g1 = 2 * tile + 2 < G ? 2 * tile + 2 : G;          // groups [g0, g1) are this workgroup's
+            for (int i = tid; i < 32 * NB * kHeadSlots; i += kMainThreads) {
+                const int r = i / kHeadSlots, sl = i % kHeadSlots;
+                const int64_t row = b0 + r, grp = 2 * wt + sl;
+                if (row < B && grp >= g0 && grp < g1) a.heads[row * G + grp] = hbuf[i];
             }
         }
     });
