@@ -18,6 +18,8 @@ see into, so the required wait states are checked here on its output:
     least 2 wait states later;
   - the accumulators stay in place: no AGPR moves or copies inside the d-step
     loop (the pattern the builtin MFMAs fall into at this register pressure).
+And one schedule property: after each d-step's barrier, the previous step's
+16 deferred MFMAs issue before the first wait for an LDS read.
 """
 import os
 import re
@@ -80,6 +82,23 @@ def test_dstep_loop_has_no_waterfall(asm, dt, sample, tail):
         assert "s_and_saveexec" not in blk and "v_readfirstlane" not in blk, blk[:400]
         # one buffer load to LDS per 16-byte chunk of the step: 32 per two d-steps
         assert blk.count("buffer_load_dwordx4") <= 32
+
+
+@pytest.mark.parametrize("dt", [0, 1, 2])
+@pytest.mark.parametrize("sample", [False, True])
+@pytest.mark.parametrize("tail", [False, True])
+def test_deferred_mfmas_follow_each_barrier(asm, dt, sample, tail):
+    """Each d-step's barrier is followed by the previous step's 16 deferred
+    MFMAs before the first wait for an LDS read: the matrix cores work while
+    the step's first operand reads land.  A wait hoisted above them would
+    leave the results right and the d-steps ~2-3 % slower."""
+    body, _ = _kernel(asm, dt, sample, tail)
+    blocks = [b for b in re.split(r"\n(?=\.LBB\d+_\d+:)", body) if b.count("v_mfma") >= 256]
+    assert len(blocks) == 1, "one block holds the two-step loop body"
+    steps = blocks[0].split("s_barrier")[1:3]   # the loop body's two d-steps
+    assert len(steps) == 2
+    for st in steps:
+        assert re.split(r"s_waitcnt[^\n]*lgkmcnt", st)[0].count("v_mfma") == 16
 
 
 @pytest.mark.parametrize("dt", [0, 1, 2])
