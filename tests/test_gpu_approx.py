@@ -239,3 +239,30 @@ def test_approx_candidates_truncated_ties(cuda_dev, c):
     Vo, Io, cvo, cio = oracle.approx(Xn, Wn, bn, k, c, with_candidates=True)
     assert np.array_equal(cb.cpu().numpy(), cvo)
     assert np.array_equal(V.cpu().numpy(), Vo) and np.array_equal(I.cpu().numpy(), Io)
+
+
+def test_candidate_heads_across_workgroup_runs(cuda_dev):
+    """group_kernel collects each row's group heads in LDS over windows of 8
+    aligned tiles and writes a window when it ends or when the workgroup's
+    run of tiles does.  Here a run is 11 tiles on a 256-CU device (windows
+    straddle the runs), the group count is odd and the last group partial.
+    Two calls on one stream with different inputs: a head the flush missed
+    would be the first call's, and cand_kernel, which skips groups by their
+    heads, would then miss top-k latents of the second."""
+    B, d, k, c = 40, 64, 16, 16
+    G = 5621                          # 2811 tiles: 11 per workgroup over 256 workgroups
+    F = G * 128 - 50
+    print(f"case approx heads across runs B={B} F={F}", flush=True)
+    nt = (F + 127) // 128
+    for seed in (41, 42):
+        X, W, b = make_inputs(B, d, F, torch.bfloat16, seed=seed, device=cuda_dev)
+        cb = torch.empty((B, nt, c), dtype=torch.float32, device=cuda_dev)
+        V, I = topk_sae_cuda_approx(X, W, b, k, c, candidate_buffer=cb)
+        Ve, Ie = topk_sae_cuda_exact(X, W, b, k)
+        assert torch.equal(V, Ve) and torch.equal(I, Ie), f"seed {seed}"
+    _, _, cvo, cio = oracle.approx(_np(X), _np(W), _np(b), k, c, with_candidates=True)
+    cbn = cb.cpu().numpy()
+    pad = cio < 0
+    assert np.array_equal(cbn[pad], cvo[pad])
+    err = np.abs(cbn[~pad] - cvo[~pad]) / np.maximum(np.abs(cvo[~pad]), 1.0)
+    assert err.max() <= 2e-3
